@@ -1,0 +1,309 @@
+#!/usr/bin/env python3
+"""Benchmark of the full-attention KV-cache decode path on one MI355X.
+
+Default workload (config 3 of the measurement plan): ragged batched decode,
+B=32 sequences with cached lengths U[1024, 8192] (seed 0), 16 full-attention
+layers of 24 query / 4 KV heads x 256 dims, FP16 cache in 16-token pages with
+randomly permuted page ids.  One step = one decode step of the whole stack:
+the step plan upload, then per layer the fused QK-norm+RoPE+K/V append and
+the split-K GQA decode attention.  After each step the lengths are set back,
+so every timed step is the same workload (append at position L_b, attend
+over L_b+1 rows).
+
+Prints ONE JSON line.  ``value`` is the KV bytes the decode attention reads
+per second over the whole timed region (the metric's "decode-attn KV-read
+HBM GB/s"); ``tok_per_s`` is sequences x steps / time.  ``roofline`` is the
+decode kernel alone: algorithmic bytes per launch (KV rows read + queries)
+over its average duration from HIP events recorded on the launch stream
+around each decode launch inside the timed region.  ``cpu_baseline`` is the
+numpy oracle on a bounded sample of the same workload on this host.
+
+Other workloads: --workload ctx8192 (every sequence at 8192 rows), c2
+(16 layers, B=1, 128 decode steps growing 128 -> 256 rows), copy (HBM
+stream-copy probe: the measured bandwidth ceiling).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from mi50grad_amd import _lib  # noqa: E402
+from mi50grad_amd.device import Event, GPUDevice  # noqa: E402
+from mi50grad_amd.kv_cache import PagedKVCache  # noqa: E402
+from mi50grad_amd.rope import rope_tables  # noqa: E402
+from mi50grad_amd import workloads as wl  # noqa: E402
+
+H, HKV, D, LAYERS = 24, 4, 256, 16
+HBM_PEAK_GBS = 8000.0
+ROW_BYTES = 2 * HKV * D * 2  # K + V of one token in one layer
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def fill_pools(dev: GPUDevice, cache: PagedKVCache, n_blocks: int, seed: int = 0) -> None:
+    """Fill every layer's K/V pages [0, n_blocks) with N(0,1) fp16 data.
+
+    A 64 MiB random tile is drawn on the host once and tiled on the device
+    (values only matter for realism; timings do not depend on them)."""
+    rng = np.random.default_rng(seed)
+    tile = rng.standard_normal(32 * 1024 * 1024, dtype=np.float32).astype(np.float16)
+    d_tile = dev.array(tile)
+    need = n_blocks * cache.block_bytes
+    for layer in range(cache.n_layers):
+        for base in cache.layer_pools(layer):
+            off = 0
+            while off < need:
+                n = min(tile.nbytes, need - off)
+                _lib.call("kva_memcpy_d2d", base + off, d_tile.ptr, n)
+                off += n
+    d_tile.free()
+
+
+def make_inputs(dev: GPUDevice, n_tok: int, seed: int = 1):
+    rng = np.random.default_rng(seed)
+    per_layer = []
+    for _ in range(LAYERS):
+        q = dev.array(wl.normal_f16(rng, (n_tok, H, D)))
+        k = dev.array(wl.normal_f16(rng, (n_tok, HKV, D)))
+        v = dev.array(wl.normal_f16(rng, (n_tok, HKV, D)))
+        qw = dev.array(wl.norm_weight(rng))
+        kw = dev.array(wl.norm_weight(rng))
+        out = dev.empty((n_tok, H, D), np.float16)
+        per_layer.append((q, k, v, qw, kw, out))
+    return per_layer
+
+
+def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, label):
+    B = len(lengths)
+    mbps = max(len(ids) for ids in block_ids)
+    cache = PagedKVCache(n_layers=LAYERS, max_seqs=B, max_blocks=n_blocks, max_blocks_per_seq=mbps,
+                         max_step_tokens=max(64, B))
+    for b, ids in enumerate(block_ids):
+        cache.set_blocks(b, ids)
+    cache.sync_tables()
+    fill_pools(dev, cache, n_blocks)
+    if split:
+        cache.set_decode_split(split)
+    rows = int(max(lengths)) + 2
+    cos, sin = rope_tables(rows)
+    d_cos, d_sin = dev.array(cos), dev.array(sin)
+    inputs = make_inputs(dev, B)
+    seqs = list(range(B))
+    ones = [1] * B
+
+    def step(ev_pairs=None):
+        for b in seqs:
+            cache.set_len(b, int(lengths[b]))
+        cache.begin_step(seqs, ones)
+        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
+            if ev_pairs is not None:
+                ev_pairs[layer][0].record()
+            cache.decode(layer, q, out)
+            if ev_pairs is not None:
+                ev_pairs[layer][1].record()
+
+    log(f"{label}: B={B} sum_ctx={int(np.sum(lengths)) + B} warmup={warmup}")
+    for _ in range(warmup):
+        step()
+    dev.synchronize()
+    split_used, n_splits = cache.decode_split()
+    evs = [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    dec_ms = [e[0].elapsed_ms(e[1]) for per_step in evs for e in per_step]
+    for per_step in evs:
+        for a, b in per_step:
+            a.destroy()
+            b.destroy()
+    log(f"{label}: {steps} steps in {wall * 1e3:.2f} ms; decode kernel avg {np.mean(dec_ms) * 1e3:.1f} us")
+    cache.destroy()
+    ctx = np.asarray(lengths, dtype=np.int64) + 1
+    by = wl.decode_bytes(ctx)
+    return {
+        "wall_s": wall, "steps": steps, "B": B,
+        "kv_bytes_per_layer": by["kv"], "alg_bytes_decode_launch": by["kv"] + by["q"],
+        "alg_bytes_layer_step": by["kv"] + by["q"] + by["out"] + by["append"],
+        "decode_avg_us": float(np.mean(dec_ms) * 1e3), "decode_min_us": float(np.min(dec_ms) * 1e3),
+        "split_tokens": split_used, "n_splits": n_splits,
+    }
+
+
+def c2_workload(dev, steps_unused, warmup):
+    """Config 2: B=1, 16 layers, 128 decode steps from a 128-row cache."""
+    B, start, n_steps = 1, 128, 128
+    cache = PagedKVCache(n_layers=LAYERS, max_seqs=1, max_blocks=16, max_blocks_per_seq=16,
+                         max_step_tokens=16)
+    cache.reserve(0, 256)
+    cache.sync_tables()
+    fill_pools(dev, cache, 16)
+    cos, sin = rope_tables(256)
+    d_cos, d_sin = dev.array(cos), dev.array(sin)
+    inputs = make_inputs(dev, B)
+
+    def run():
+        cache.set_len(0, start)
+        for _ in range(n_steps):
+            cache.begin_step([0], [1])
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 256)
+                cache.decode(layer, q, out)
+
+    for _ in range(max(1, warmup)):
+        run()
+    dev.synchronize()
+    t0 = time.perf_counter()
+    run()
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    cache.destroy()
+    kv = LAYERS * ROW_BYTES * sum(range(start + 1, start + n_steps + 1))
+    return {"wall_s": wall, "steps": n_steps, "kv_bytes": kv}
+
+
+def copy_probe(dev, gib: float = 4.0, reps: int = 20):
+    n = int(gib * (1 << 30)) // 16 * 16
+    a, b = dev.malloc(n), dev.malloc(n)
+    _lib.call("kva_memset", a, 0, n)
+    s, e = Event(), Event()
+    for _ in range(3):
+        _lib.call("kva_hbm_copy", b, a, n, None)
+    s.record()
+    for _ in range(reps):
+        _lib.call("kva_hbm_copy", b, a, n, None)
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_ms(e) / reps
+    dev.free(a)
+    dev.free(b)
+    return {"bytes_per_launch": 2 * n, "avg_us": ms * 1e3, "gbs": 2 * n / (ms * 1e-3) / 1e9}
+
+
+def cpu_baseline(budget_s: float = 10.0):
+    """The numpy oracle's decode attention on a slice of the config-3 workload.
+
+    Sample: the first 4 sequences of config 3 (seed 0), one layer, one decode
+    step (append excluded), single-threaded BLAS; repeated until ~budget_s.
+    Reported as KV GB/s with the same algorithmic byte count as the GPU row."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import kvattn_oracle as orc
+
+    spec = wl.c3_spec(0)
+    lens = [int(x) + 1 for x in spec.lengths[:4]]
+    rng = np.random.default_rng(3)
+    q = wl.normal_f16(rng, (len(lens), H, D))
+    ks = [wl.normal_f16(rng, (n, HKV, D)) for n in lens]
+    vs = [wl.normal_f16(rng, (n, HKV, D)) for n in lens]
+    reps, t = 0, 0.0
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        while t < budget_s:
+            orc.decode_attention(q, ks, vs)
+            reps += 1
+            t = time.perf_counter() - t0
+    kv = sum(lens) * ROW_BYTES * reps
+    return {"value": kv / t / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle decode_attention, config-3 sequences 0-3 "
+                      f"(ctx {lens}), one layer, {reps} reps in {t:.1f} s, 1 BLAS thread; "
+                      f"host {os.cpu_count()} logical CPUs"}
+
+
+def load_traffic(name: str):
+    p = ROOT / "profiles" / name
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "copy"])
+    ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build runs the path on a single MI355X "
+              "(see the sharding design); run it with --gpus 1", file=sys.stderr)
+        return 2
+    dev = GPUDevice(0)
+
+    if args.workload == "copy":
+        r = copy_probe(dev)
+        print(json.dumps({"metric": "HBM stream copy GB/s", "value": r["gbs"], "unit": "GB/s",
+                          "n_gpus": 1, "avg_us": r["avg_us"], "bytes_per_launch": r["bytes_per_launch"],
+                          "higher_is_better": True}))
+        return 0
+    if args.workload == "c2":
+        r = c2_workload(dev, args.steps, args.warmup)
+        ms = r["wall_s"] * 1e3 / r["steps"]
+        print(json.dumps({"metric": "config-2 decode step time (16 layers, B=1, 128->256 rows)",
+                          "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": r["steps"],
+                          "ms_per_step": ms, "higher_is_better": False,
+                          "kv_gbs": r["kv_bytes"] / r["wall_s"] / 1e9, "dtype": "f16",
+                          "data": "synthetic", "config": {"workload": "C2"}}))
+        return 0
+
+    if args.workload == "c3":
+        spec = wl.c3_spec(0)
+        lengths, ids, nb = spec.lengths, spec.block_ids, spec.n_blocks
+        workload = ("C3 ragged batched decode: B=32, cached rows U[1024,8192] (seed 0), append 1 row "
+                    "per sequence then attend over L+1; 16 layers, 24 q / 4 kv heads, d=256, fp16 "
+                    "16-token pages with permuted ids")
+    else:
+        lengths = np.full(32, 8192)
+        nblk = (8192 + 1 + 15) // 16
+        perm = np.random.default_rng(0).permutation(32 * nblk)
+        ids = [[int(x) for x in perm[b * nblk:(b + 1) * nblk]] for b in range(32)]
+        nb = 32 * nblk
+        workload = ("C3 at fixed ctx: B=32, every sequence 8192 cached rows, append 1 then attend over "
+                    "8193; 16 layers, 24 q / 4 kv heads, d=256, fp16 16-token pages, permuted ids")
+    r = decode_workload(dev, lengths, ids, nb, args.steps, args.warmup, args.split, args.workload)
+    kv_total = r["kv_bytes_per_layer"] * LAYERS * r["steps"]
+    value = kv_total / r["wall_s"] / 1e9
+    ms_step = r["wall_s"] * 1e3 / r["steps"]
+    achieved = r["alg_bytes_decode_launch"] / (r["decode_avg_us"] * 1e-6) / 1e9
+    line = {
+        "metric": "decode-attn KV-read HBM GB/s (% of MI355X peak) + tok/s at B=32, ctx=8192",
+        "value": value, "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
+        "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": workload, "layers": LAYERS, "batch": r["B"],
+                   "split_tokens": r["split_tokens"], "n_splits": r["n_splits"]},
+        "pct_of_hbm_peak": 100.0 * value / HBM_PEAK_GBS,
+        "tok_per_s": r["B"] * r["steps"] / r["wall_s"],
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": load_traffic(f"decode_{args.workload}_traffic.json"),
+                     "kernel": "decode_kernel<6>", "avg_us": r["decode_avg_us"],
+                     "alg_bytes_per_launch": r["alg_bytes_decode_launch"]},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (numpy oracle, ~10 s)")
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,253 @@
+/*
+ * kvattn.h — C ABI of libkvattn.so, the MI355X (gfx950) full-attention
+ * KV-cache path: paged FP16 K/V cache, fused QK-RMSNorm + RoPE + K/V append,
+ * split-K GQA decode, chunked causal prefill and tree-verify attention.
+ *
+ * Conventions (the reference's host wrappers use the same ones):
+ *   - every pointer argument named q, k, v, out, x, w, cos_*, sin_*, *_base,
+ *     cache_dst is a DEVICE address; index arrays (seq_ids, n_new, ...) are
+ *     HOST arrays unless stated otherwise;
+ *   - fp16 tensors are passed as void* (IEEE binary16, little endian);
+ *   - every call returns int: 0 = ok, > 0 = hipError_t from the HIP runtime,
+ *     < 0 = one of the KVA_ERR_* validation codes below; kva_last_error_string
+ *     gives detail for the calling thread; there are no silent fallbacks;
+ *   - kva_stream_t is a hipStream_t (NULL = the legacy default stream); a
+ *     cache is driven from one host thread and its calls are ordered on the
+ *     stream they are given: calls on different streams must be ordered by
+ *     the caller;
+ *   - the library allocates device memory only in kva_create and the
+ *     kva_dev_* helpers, never inside a hot-path call.
+ *
+ * Reference citations are to larkinwc/mi50grad (file:line).
+ */
+#ifndef KVATTN_H
+#define KVATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *kva_stream_t;
+typedef void *kva_event_t;
+typedef struct kva_cache kva_cache;
+
+enum {
+    KVA_OK = 0,
+    KVA_ERR_INVALID_ARG = -1,   /* null pointer, negative count, bad index  */
+    KVA_ERR_UNSUPPORTED = -2,   /* shape outside what the kernels implement */
+    KVA_ERR_NO_DEVICE = -3,     /* device call on a host-only cache         */
+    KVA_ERR_OUT_OF_BLOCKS = -4, /* block pool exhausted                     */
+    KVA_ERR_CAPACITY = -5,      /* length beyond max_blocks_per_seq * 16    */
+    KVA_ERR_BAD_SEQ = -6,       /* sequence id out of range / not active    */
+    KVA_ERR_BAD_BLOCK = -7,     /* block id out of range or already in use  */
+    KVA_ERR_STATE = -8,         /* call order (no step begun, wrong mode)   */
+    KVA_ERR_ROLLBACK = -9,      /* rollback past the base / unsorted rows   */
+    KVA_ERR_MISALIGNED = -10,   /* device pointer not 16-byte aligned       */
+    KVA_ERR_DOUBLE_FREE = -11   /* sequence freed twice                     */
+};
+
+/* Cache flags. */
+#define KVA_FLAG_HOST_ONLY 0x1u /* no device memory: host bookkeeping only  */
+
+/*
+ * Cache configuration.  Replaces the constructor arguments of
+ * KVCache(config, max_seq_len, device, tp_size, batch_size), engine.py:88-117,
+ * whose contiguous [layers][batch][max_seq][kv_heads][256] layout becomes a
+ * pool of 16-token pages per layer: [max_blocks][16][num_kv_heads][head_dim].
+ */
+typedef struct kva_config {
+    int32_t n_layers;           /* full-attention layers held (16)          */
+    int32_t num_heads;          /* query heads (24)                         */
+    int32_t num_kv_heads;       /* KV heads (4); num_heads % this == 0      */
+    int32_t head_dim;           /* 256 (the only supported value)           */
+    int32_t rotary_dim;         /* 64; RoPE on interleaved pairs of [0,64)  */
+    int32_t block_tokens;       /* 16 (the only supported value)            */
+    int32_t max_seqs;           /* sequence slots                           */
+    int32_t max_blocks;         /* physical blocks in each layer's pool     */
+    int32_t max_blocks_per_seq; /* block-table width                        */
+    int32_t max_step_tokens;    /* most new tokens in one step, all seqs    */
+    float eps;                  /* RMSNorm epsilon (1e-6)                   */
+    uint32_t flags;             /* KVA_FLAG_*                               */
+} kva_config;
+
+/* Byte layout of the pools, for callers that address rows themselves. */
+typedef struct kva_layout {
+    uint64_t row_bytes;   /* one token, all KV heads: kv_heads*head_dim*2   */
+    uint64_t block_bytes; /* block_tokens * row_bytes                       */
+    uint64_t layer_bytes; /* max_blocks * block_bytes (per K or V pool)     */
+    int32_t block_tokens;
+    int32_t max_blocks_per_seq;
+} kva_layout;
+
+/* ---- lifetime ---------------------------------------------------------- */
+/* KVCache.__init__ (engine.py:88-117) and cleanup() (engine.py:288-290).   */
+int kva_create(const kva_config *cfg, kva_cache **out);
+int kva_destroy(kva_cache *cache);
+const char *kva_last_error_string(void);
+const char *kva_version(void);
+int kva_get_layout(const kva_cache *cache, kva_layout *out);
+/* Device base of layer `layer`'s K and V pools: KVCache.layer_k_ptr /
+ * layer_v_ptr (engine.py:123-156) for the paged layout.                    */
+int kva_layer_pools(const kva_cache *cache, int32_t layer, void **k_pool, void **v_pool);
+
+/* ---- host block management (no device work) ---------------------------- */
+/* Ensure sequence `seq_id` can hold n_tokens rows, taking free blocks from
+ * the pool.  The reference pre-allocates max_seq_len rows per batch slot
+ * (engine.py:101-117); here capacity grows a page at a time.               */
+int kva_seq_reserve(kva_cache *cache, int32_t seq_id, int32_t n_tokens);
+/* Give sequence `seq_id` an explicit block list (e.g. a permuted one).  The
+ * blocks must be free; the sequence's previous blocks are released.        */
+int kva_seq_set_blocks(kva_cache *cache, int32_t seq_id, const int32_t *block_ids,
+                       int32_t n_blocks);
+/* Release a sequence's blocks and set its length to 0: KVCache.reset()
+ * (engine.py:228-230) for one sequence.                                    */
+int kva_seq_free(kva_cache *cache, int32_t seq_id);
+int kva_seq_get_len(const kva_cache *cache, int32_t seq_id, int32_t *len);
+/* Set the committed length (the reference's `current_len`, engine.py:94,
+ * written by callers at engine.py:3283 and tp_engine.py:1684).  Rows at or
+ * beyond the new length become invisible; capacity must already exist.    */
+int kva_seq_set_len(kva_cache *cache, int32_t seq_id, int32_t len);
+int kva_seq_get_blocks(const kva_cache *cache, int32_t seq_id, int32_t *block_ids,
+                       int32_t cap, int32_t *n_blocks);
+int kva_free_block_count(const kva_cache *cache, int32_t *n_free);
+/* Device address of one logical row: KVCache.get_kv_ptr (engine.py:158-176).
+ * Valid for reads/writes of that single [num_kv_heads, head_dim] row.      */
+int kva_row_ptr(const kva_cache *cache, int32_t layer, int32_t seq_id, int32_t slot,
+                void **k_row, void **v_row);
+/* Push block-table changes made by kva_seq_* calls to the device.          */
+int kva_sync_tables(kva_cache *cache, kva_stream_t stream);
+
+/* ---- per-step plan ----------------------------------------------------- */
+/* Start a step that appends n_new[b] rows to each sequence seq_ids[b]
+ * (b < n_seqs; a sequence appears at most once).  New rows take slots
+ * len..len+n_new-1; the committed length becomes len+n_new (the reference
+ * writes at current_len and then calls advance(), engine.py:220-226).
+ * rope_pos (nullable, one per new token in sequence order) overrides the
+ * RoPE position, which defaults to the slot; tree verify passes
+ * len + depth.  tree_bits (nullable, one per new token) gives, for tree
+ * verify, the set of new tokens of the same sequence that token sees
+ * (bit j = j-th new token of that sequence; self and ancestors).  One
+ * host->device copy on `stream` carries the plan and any block-table
+ * changes; every layer of the step reuses it (the reference patches the
+ * same per-step arguments for all layers: c_dispatch.c:426-456).           */
+int kva_step_begin(kva_cache *cache, int32_t n_seqs, const int32_t *seq_ids,
+                   const int32_t *n_new, const int32_t *rope_pos,
+                   const uint64_t *tree_bits, kva_stream_t stream);
+
+/* ---- hot path (device work, per layer) --------------------------------- */
+/* Fused QK-RMSNorm + interleaved partial RoPE + K/V append for every new
+ * token of the step.  Replaces qknorm_rope_fused (qknorm_rope.hip:55-162)
+ * launched via _launch_qknorm_rope (engine.py:2371-2399) for Q,
+ * qknorm_rope_cachew_fused (qknorm_rope_cachew.hip:52-142) via
+ * _launch_qknorm_rope_cachew (engine.py:2401-2432) for K, and the V write
+ * into the cache slot (engine.py:2012-2018 / append_kv_gpu :199-218).
+ * q [T, num_heads, 256] and k [T, num_kv_heads, 256] are normalised and
+ * rotated in place (as the reference kernels do); K is also stored to the
+ * cache; v [T, num_kv_heads, 256] is copied to the cache.  T is the step's
+ * token count, tokens in sequence order.  cos_tab/sin_tab: [table_rows,
+ * rotary_dim/2] fp16 (the tables of _init_rope_tables, engine.py:1025-1046). */
+int kva_append_qknorm_rope(kva_cache *cache, int32_t layer, void *q, void *k,
+                           const void *v, const void *q_norm_w, const void *k_norm_w,
+                           const void *cos_tab, const void *sin_tab, int32_t table_rows,
+                           kva_stream_t stream);
+/* GQA decode attention, one query token per sequence (every n_new == 1):
+ * out[b] = softmax(q[b] K^T / 16) V over the sequence's rows [0, len).
+ * Replaces flash_attn_256_decode (flash_attn_256_tuned.hip:198-350) as
+ * launched by _launch_decode_attn_256 (engine.py:2760-2804) and the batched
+ * launcher _launch_decode_attn_256_batched (engine.py:2806-2857), now with
+ * ragged per-sequence lengths.  q, out: [n_seqs, num_heads, 256] fp16.     */
+int kva_decode(kva_cache *cache, int32_t layer, const void *q, void *out,
+               kva_stream_t stream);
+/* Causal attention of each sequence's new rows over cache + new rows: new
+ * token i (slot s) sees slots [0, s].  Replaces the prefill attention of
+ * _prefill_full_attention (engine.py:3043-3139; flash_attn_256_fp16,
+ * flash_attn_256.hip:38-137; flash_attn_256_v3_prefill,
+ * flash_attn_256_v3.hip:189-404), which could only start from an empty
+ * cache.  q, out: [T, num_heads, 256] fp16 in step token order.            */
+int kva_prefill(kva_cache *cache, int32_t layer, const void *q, void *out,
+                kva_stream_t stream);
+/* Tree-verify attention: new token i sees the cache rows [0, len_before)
+ * plus the new tokens in its tree_bits set.  Replaces flash_attn_tree_decode
+ * (flash_attn_tree.hip:72-175) under the mask of TreeAttentionMask
+ * (tree_attention.py:186-208), wired in decode_step_tree
+ * (tp_engine.py:3186-3214).  q, out: [T, num_heads, 256] fp16.            */
+int kva_tree_verify(kva_cache *cache, int32_t layer, const void *q, void *out,
+                    kva_stream_t stream);
+/* Keep accepted tree rows and drop the rest, in every layer: for sequence
+ * seq_ids[b], rows base_len[b] + keep_rows[j] (j in [keep_off[b],
+ * keep_off[b+1]), strictly increasing) move to base_len[b] + (j -
+ * keep_off[b]) and the length becomes base_len[b] + count.  Replaces
+ * rollback_kv_cache (tp_engine.py:1673-1687), which only moved the length.
+ * All index arrays are host arrays.                                        */
+int kva_rollback(kva_cache *cache, int32_t n_seqs, const int32_t *seq_ids,
+                 const int32_t *base_len, const int32_t *keep_off,
+                 const int32_t *keep_rows, kva_stream_t stream);
+
+/* Split-K tuning for kva_decode: tokens per split (multiple of 64); 0 =
+ * automatic.  Returns the value in effect through *effective.             */
+int kva_set_decode_split(kva_cache *cache, int32_t split_tokens);
+int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,
+                         int32_t *n_splits);
+
+/* ---- reference-kernel-compatible entry points (contiguous caches) ------- */
+/* qknorm_rope_fused / qknorm_rope_cachew_fused on a contiguous
+ * [num_heads, head_dim] buffer, in place; cache_dst (nullable) also gets the
+ * result (qknorm_rope.hip:55-162, qknorm_rope_cachew.hip:52-142).
+ * cos_row/sin_row point at the position's table row (the reference passes
+ * d_cos + position*half_rotary*2, engine.py:2387).  head_dim in {64, 128,
+ * 256}; half_rotary a multiple of 4 with 2*half_rotary <= head_dim.       */
+int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row,
+                           const void *sin_row, void *cache_dst, int32_t num_heads,
+                           int32_t head_dim, int32_t half_rotary, float eps,
+                           kva_stream_t stream);
+/* flash_attn_256_decode semantics (flash_attn_256_tuned.hip:198-350) on a
+ * contiguous cache K/V [kv_seq_len, num_kv_heads, 256]: one query row
+ * q [num_heads, 256] -> out [num_heads, 256].  `ws` (nullable) lends its
+ * split-K workspace; with NULL the call runs one split per KV head.        */
+int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base,
+                      const void *v_base, void *out, int32_t kv_seq_len,
+                      int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream);
+/* The intended semantics of _launch_decode_attn_256_batched
+ * (engine.py:2806-2857; its kernel ignores the batch index, survey fact F9):
+ * sequence b's contiguous cache starts at k_base/v_base + b*batch_stride
+ * bytes; q, out: [batch, num_heads, 256]; all sequences have kv_seq_len
+ * rows (the reference's shared current_len).                              */
+int kva_legacy_decode_batched(kva_cache *ws, const void *q, const void *k_base,
+                              const void *v_base, void *out, int32_t kv_seq_len,
+                              int32_t batch, int64_t batch_stride,
+                              int32_t num_heads, int32_t num_kv_heads,
+                              kva_stream_t stream);
+
+/* HBM stream-copy probe: one kernel copying `bytes` (a multiple of 16,
+ * 16-byte aligned pointers) with 16-byte lanes.  The measured-bandwidth
+ * counterpart of the reference's bench/micro/hbm_bandwidth.hip.cpp, and the
+ * known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE counters.      */
+int kva_hbm_copy(void *dst, const void *src, size_t bytes, kva_stream_t stream);
+
+/* ---- device helpers (the GPUDevice surface, hip_dispatch.py:594-703) ----- */
+int kva_dev_count(int32_t *n);
+int kva_dev_set(int32_t device);
+int kva_dev_malloc(void **ptr, size_t bytes);
+int kva_dev_free(void *ptr);
+int kva_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int kva_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int kva_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int kva_memset(void *dst, int32_t value, size_t bytes);
+int kva_dev_synchronize(void);
+int kva_stream_create(kva_stream_t *stream);
+int kva_stream_destroy(kva_stream_t stream);
+int kva_stream_synchronize(kva_stream_t stream);
+int kva_event_create(kva_event_t *ev);
+int kva_event_destroy(kva_event_t ev);
+int kva_event_record(kva_event_t ev, kva_stream_t stream);
+int kva_event_synchronize(kva_event_t ev);
+int kva_event_elapsed_ms(float *ms, kva_event_t start, kva_event_t stop);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVATTN_H */

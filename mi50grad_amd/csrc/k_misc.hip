@@ -1,0 +1,74 @@
+// Small bookkeeping kernels: block-table patches and tree rollback moves.
+#include "k_common.h"
+#include "kva_internal.h"
+
+#include <algorithm>
+
+namespace kva {
+namespace {
+
+__global__ void table_patch_kernel(int32_t *table, int32_t stride, const int32_t *patches,
+                                   int32_t n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int32_t seq = patches[3 * i];
+    const int32_t idx = patches[3 * i + 1];
+    table[static_cast<size_t>(seq) * stride + idx] = patches[3 * i + 2];
+}
+
+// grid (sequence group, layer, K|V).  The moves of one sequence run in order
+// and each thread copies the same 16-byte columns of every row, so a row read
+// by an earlier move is read before a later move overwrites it (accepted
+// rows only move towards lower slots: dst = k <= keep[k] = src).
+__global__ __launch_bounds__(256) void rollback_kernel(RollbackArgs a) {
+    const int grp = blockIdx.x;
+    const int layer = blockIdx.y;
+    uint16_t *pool = (blockIdx.z == 0 ? a.k_pools : a.v_pools) + a.layer_elems * layer;
+    const size_t row_elems = static_cast<size_t>(a.num_kv_heads) * kHeadDim;
+    for (int mv = a.move_off[grp]; mv < a.move_off[grp + 1]; ++mv) {
+        const int32_t seq = a.moves[3 * mv];
+        const int32_t src = a.moves[3 * mv + 1];
+        const int32_t dst = a.moves[3 * mv + 2];
+        const int32_t *trow = a.table + static_cast<size_t>(seq) * a.table_stride;
+        const uint16_t *ps =
+            pool + (static_cast<size_t>(trow[src >> 4]) * kBlockTokens + (src & 15)) * row_elems;
+        uint16_t *pd =
+            pool + (static_cast<size_t>(trow[dst >> 4]) * kBlockTokens + (dst & 15)) * row_elems;
+        for (size_t e = 8 * threadIdx.x; e < row_elems; e += 8 * blockDim.x) st16(pd + e, ld16(ps + e));
+    }
+}
+
+// Plain streaming copy, 16 bytes per lane per step, grid-stride.
+__global__ __launch_bounds__(256) void copy_kernel(uint4 *__restrict__ dst,
+                                                   const uint4 *__restrict__ src, size_t n16) {
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        dst[i] = src[i];
+}
+
+}  // namespace
+
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    const size_t n16 = bytes / 16;
+    if (n16 == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((n16 + 255) / 256, 256 * 32);
+    hipLaunchKernelGGL(copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s,
+                       static_cast<uint4 *>(dst), static_cast<const uint4 *>(src), n16);
+    return hipGetLastError();
+}
+
+hipError_t launch_table_patch(int32_t *table, int32_t stride, const int32_t *patches,
+                              int32_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(table_patch_kernel, dim3((n + 255) / 256), dim3(256), 0, s, table, stride,
+                       patches, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_rollback(const RollbackArgs &a, hipStream_t s) {
+    if (a.n_groups <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rollback_kernel, dim3(a.n_groups, a.n_layers, 2), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace kva

@@ -1,0 +1,1019 @@
+// Host side of libkvattn: the paged block pool, per-sequence block tables and
+// lengths, per-step plans, argument validation and the C ABI of kvattn.h.
+// Built with g++ against the HIP runtime API; kernels live in k_*.hip.
+//
+// Reference behaviour restated here:
+//   - KVCache (engine.py:79-291): one contiguous [max_seq][kv_heads][256]
+//     region per layer and batch slot, one shared current_len; here a pool of
+//     16-token pages per layer with a block table and a length per sequence.
+//   - the C dispatch loop's per-step argument patching (c_dispatch.c:426-456,
+//     used at :1066-1103): here one host->device copy of a step plan that all
+//     layers of the step read.
+//   - HIP errors raise (hip_dispatch.py:267-269) -> here every call returns a
+//     code and kva_last_error_string() says why; no silent fallbacks.
+#include "../../include/kvattn.h"
+#include "kva_internal.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(static_cast<int>(e), "%s: %s (hipError %d)", what, hipGetErrorString(e),
+                static_cast<int>(e));
+}
+
+#define KVA_HIP(call)                                         \
+    do {                                                      \
+        hipError_t e_ = (call);                               \
+        if (e_ != hipSuccess) return hip_fail(e_, #call);     \
+    } while (0)
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int kStageSlots = 4;
+constexpr int kTargetDecodeUnits = 2048;  // workgroups a decode launch aims for
+
+}  // namespace
+
+struct kva_cache {
+    kva_config cfg{};
+    bool host_only = false;
+    int group = 0;  // query heads per KV head
+    size_t row_elems = 0;
+    size_t layer_elems = 0;
+
+    // device memory
+    uint16_t *d_k = nullptr;
+    uint16_t *d_v = nullptr;
+    int32_t *d_table = nullptr;
+    uint8_t *d_step = nullptr;
+    size_t step_bytes = 0;
+    uint8_t *d_aux = nullptr;
+    size_t aux_bytes = 0;
+    float *d_ws_acc = nullptr;
+    float *d_ws_ml = nullptr;
+    int32_t *d_counters = nullptr;  // [max_seqs][num_kv_heads] split arrivals
+    int32_t ws_max_splits = 0;
+
+    // pinned staging ring
+    uint8_t *h_stage[kStageSlots] = {};
+    hipEvent_t ev[kStageSlots] = {};
+    bool ev_live[kStageSlots] = {};
+    int stage_next = 0;
+    size_t stage_bytes = 0;
+
+    // host bookkeeping
+    std::vector<int32_t> table;   // [max_seqs][max_blocks_per_seq]
+    std::vector<int32_t> nblk;    // blocks held per sequence
+    std::vector<int32_t> len;     // committed length per sequence
+    std::vector<uint8_t> freed;   // sequence released by kva_seq_free
+    std::vector<uint8_t> used;    // per block
+    std::vector<int32_t> free_list;
+    std::vector<int32_t> patches; // pending (seq, idx, block) triples
+
+    // current step plan
+    bool step_valid = false;
+    int32_t st_n_seqs = 0, st_n_tok = 0, st_max_ctx = 0, st_max_new = 0, st_max_pos = 0;
+    int64_t st_sum_ctx = 0;
+    bool st_all_one = false, st_has_bits = false;
+    size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
+           off_tslot = 0, off_tpos = 0, off_bits = 0;
+
+    int32_t split_user = 0;
+    int32_t last_split = 0, last_nsplits = 0;
+};
+
+namespace {
+
+int check_cfg(const kva_config *c) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "config is NULL");
+    if (c->n_layers <= 0 || c->max_seqs <= 0 || c->max_blocks <= 0 ||
+        c->max_blocks_per_seq <= 0 || c->max_step_tokens <= 0)
+        return fail(KVA_ERR_INVALID_ARG, "n_layers, max_seqs, max_blocks, max_blocks_per_seq and "
+                                         "max_step_tokens must be positive");
+    if (c->head_dim != kva::kHeadDim)
+        return fail(KVA_ERR_UNSUPPORTED, "head_dim %d unsupported (only 256)", c->head_dim);
+    if (c->block_tokens != kva::kBlockTokens)
+        return fail(KVA_ERR_UNSUPPORTED, "block_tokens %d unsupported (only 16)", c->block_tokens);
+    if (c->num_heads <= 0 || c->num_kv_heads <= 0 || c->num_heads % c->num_kv_heads != 0)
+        return fail(KVA_ERR_INVALID_ARG, "num_heads %d must be a positive multiple of num_kv_heads %d",
+                    c->num_heads, c->num_kv_heads);
+    const int g = c->num_heads / c->num_kv_heads;
+    if (!(g == 1 || g == 2 || g == 3 || g == 4 || g == 6 || g == 8))
+        return fail(KVA_ERR_UNSUPPORTED, "GQA group %d unsupported (1,2,3,4,6,8)", g);
+    if (c->rotary_dim < 0 || c->rotary_dim > c->head_dim || c->rotary_dim % 8 != 0)
+        return fail(KVA_ERR_UNSUPPORTED, "rotary_dim %d must be a multiple of 8 in [0, head_dim]",
+                    c->rotary_dim);
+    if (!(c->eps >= 0.0f)) return fail(KVA_ERR_INVALID_ARG, "eps must be >= 0");
+    if (static_cast<int64_t>(c->max_blocks_per_seq) * kva::kBlockTokens > (1 << 30))
+        return fail(KVA_ERR_INVALID_ARG, "max_blocks_per_seq too large");
+    return KVA_OK;
+}
+
+int check_seq(const kva_cache *c, int32_t seq) {
+    if (seq < 0 || seq >= c->cfg.max_seqs)
+        return fail(KVA_ERR_BAD_SEQ, "sequence id %d out of range [0, %d)", seq, c->cfg.max_seqs);
+    return KVA_OK;
+}
+
+// Take free blocks until `seq` holds `need` blocks.
+int grow_seq(kva_cache *c, int32_t seq, int32_t need) {
+    if (need > c->cfg.max_blocks_per_seq)
+        return fail(KVA_ERR_CAPACITY, "sequence %d needs %d blocks > max_blocks_per_seq %d", seq,
+                    need, c->cfg.max_blocks_per_seq);
+    const int32_t have = c->nblk[seq];
+    if (need <= have) return KVA_OK;
+    if (static_cast<size_t>(need - have) > c->free_list.size())
+        return fail(KVA_ERR_OUT_OF_BLOCKS, "pool exhausted: sequence %d needs %d more blocks, %zu free",
+                    seq, need - have, c->free_list.size());
+    for (int32_t i = have; i < need; ++i) {
+        const int32_t blk = c->free_list.back();
+        c->free_list.pop_back();
+        c->used[blk] = 1;
+        c->table[static_cast<size_t>(seq) * c->cfg.max_blocks_per_seq + i] = blk;
+        c->patches.insert(c->patches.end(), {seq, i, blk});
+    }
+    c->nblk[seq] = need;
+    c->freed[seq] = 0;
+    return KVA_OK;
+}
+
+void release_blocks(kva_cache *c, int32_t seq) {
+    const size_t base = static_cast<size_t>(seq) * c->cfg.max_blocks_per_seq;
+    for (int32_t i = 0; i < c->nblk[seq]; ++i) {
+        const int32_t blk = c->table[base + i];
+        c->used[blk] = 0;
+        c->free_list.push_back(blk);
+        c->table[base + i] = -1;
+    }
+    c->nblk[seq] = 0;
+}
+
+// Next pinned staging slot, waiting until its previous copy has completed.
+int acquire_stage(kva_cache *c, uint8_t **slot, int *idx) {
+    const int i = c->stage_next;
+    c->stage_next = (i + 1) % kStageSlots;
+    if (c->ev_live[i]) {
+        KVA_HIP(hipEventSynchronize(c->ev[i]));
+        c->ev_live[i] = false;
+    }
+    *slot = c->h_stage[i];
+    *idx = i;
+    return KVA_OK;
+}
+
+int release_stage(kva_cache *c, int idx, hipStream_t s) {
+    KVA_HIP(hipEventRecord(c->ev[idx], s));
+    c->ev_live[idx] = true;
+    return KVA_OK;
+}
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Upload pending block-table patches, in chunks that fit a staging slot.
+int flush_patches(kva_cache *c, hipStream_t s) {
+    if (c->host_only) {
+        c->patches.clear();
+        return KVA_OK;
+    }
+    const size_t per_chunk = c->aux_bytes / (3 * sizeof(int32_t));
+    size_t done = 0;
+    const size_t total = c->patches.size() / 3;
+    while (done < total) {
+        const size_t n = std::min(per_chunk, total - done);
+        uint8_t *h;
+        int idx;
+        int rc = acquire_stage(c, &h, &idx);
+        if (rc) return rc;
+        std::memcpy(h, c->patches.data() + 3 * done, n * 3 * sizeof(int32_t));
+        KVA_HIP(hipMemcpyAsync(c->d_aux, h, n * 3 * sizeof(int32_t), hipMemcpyHostToDevice, s));
+        rc = release_stage(c, idx, s);
+        if (rc) return rc;
+        KVA_HIP(kva::launch_table_patch(c->d_table, c->cfg.max_blocks_per_seq,
+                                        reinterpret_cast<const int32_t *>(c->d_aux),
+                                        static_cast<int32_t>(n), s));
+        done += n;
+    }
+    c->patches.clear();
+    return KVA_OK;
+}
+
+int require_device(const kva_cache *c) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (c->host_only) return fail(KVA_ERR_NO_DEVICE, "cache was created host-only");
+    return KVA_OK;
+}
+
+int check_layer(const kva_cache *c, int32_t layer) {
+    if (layer < 0 || layer >= c->cfg.n_layers)
+        return fail(KVA_ERR_INVALID_ARG, "layer %d out of range [0, %d)", layer, c->cfg.n_layers);
+    return KVA_OK;
+}
+
+template <class T>
+T *at(uint8_t *base, size_t off) {
+    return reinterpret_cast<T *>(base + off);
+}
+
+// Choose tokens per split and the split count for a decode launch.
+void choose_split(const kva_cache *c, int32_t max_ctx, int64_t sum_ctx, int32_t *split,
+                  int32_t *n_splits) {
+    const int64_t q = kva::kSplitQuantum;
+    int64_t s;
+    if (c->split_user > 0) {
+        s = c->split_user;
+    } else {
+        s = (sum_ctx * c->cfg.num_kv_heads + kTargetDecodeUnits - 1) / kTargetDecodeUnits;
+        s = std::max<int64_t>(q, std::min<int64_t>(4096, (s + q - 1) / q * q));
+    }
+    int64_t ns = (max_ctx + s - 1) / s;
+    if (ns > c->ws_max_splits) {
+        s = (max_ctx + c->ws_max_splits - 1) / c->ws_max_splits;
+        s = (s + q - 1) / q * q;
+        ns = (max_ctx + s - 1) / s;
+    }
+    *split = static_cast<int32_t>(s);
+    *n_splits = static_cast<int32_t>(std::max<int64_t>(1, ns));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *kva_last_error_string(void) { return g_err.c_str(); }
+const char *kva_version(void) { return "kvattn 0.1 gfx950"; }
+
+int kva_create(const kva_config *cfg, kva_cache **out) {
+    if (!out) return fail(KVA_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    int rc = check_cfg(cfg);
+    if (rc) return rc;
+    kva_cache *c = new kva_cache();
+    c->cfg = *cfg;
+    c->host_only = (cfg->flags & KVA_FLAG_HOST_ONLY) != 0;
+    c->group = cfg->num_heads / cfg->num_kv_heads;
+    c->row_elems = static_cast<size_t>(cfg->num_kv_heads) * cfg->head_dim;
+    c->layer_elems = static_cast<size_t>(cfg->max_blocks) * kva::kBlockTokens * c->row_elems;
+    const size_t mbps = cfg->max_blocks_per_seq;
+    c->table.assign(static_cast<size_t>(cfg->max_seqs) * mbps, -1);
+    c->nblk.assign(cfg->max_seqs, 0);
+    c->len.assign(cfg->max_seqs, 0);
+    c->freed.assign(cfg->max_seqs, 0);
+    c->used.assign(cfg->max_blocks, 0);
+    c->free_list.resize(cfg->max_blocks);
+    for (int32_t i = 0; i < cfg->max_blocks; ++i) c->free_list[i] = cfg->max_blocks - 1 - i;
+    // Split-K workspace: splits of at least 256 tokens always fit.
+    c->ws_max_splits = static_cast<int32_t>(std::max<size_t>(16, (mbps * kva::kBlockTokens + 255) / 256));
+    // Step plan: 4 per-sequence arrays + offsets + 3 per-token arrays + bits.
+    c->step_bytes = round_up(sizeof(int32_t) * (4 * static_cast<size_t>(cfg->max_seqs) + 1), 256) +
+                    round_up(sizeof(int32_t) * 3 * static_cast<size_t>(cfg->max_step_tokens), 256) +
+                    round_up(sizeof(uint64_t) * static_cast<size_t>(cfg->max_step_tokens), 256) + 1024;
+    const size_t patch_cap = std::max<size_t>(4096, cfg->max_seqs + cfg->max_step_tokens);
+    c->aux_bytes = round_up(std::max(patch_cap * 3 * sizeof(int32_t),
+                                     (static_cast<size_t>(cfg->max_step_tokens) * 3 + cfg->max_seqs + 1) *
+                                         sizeof(int32_t)),
+                            256);
+    c->stage_bytes = std::max(c->step_bytes, c->aux_bytes);
+    if (!c->host_only) {
+        auto cleanup = [&](int code) {
+            kva_destroy(c);
+            return code;
+        };
+        hipError_t e;
+        const size_t pool_bytes = c->layer_elems * cfg->n_layers * sizeof(uint16_t);
+        if ((e = hipMalloc(&c->d_k, pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(K pool)"));
+        if ((e = hipMalloc(&c->d_v, pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(V pool)"));
+        // Zeroed pools: rows never written read as finite zeros.
+        if ((e = hipMemset(c->d_k, 0, pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(K)"));
+        if ((e = hipMemset(c->d_v, 0, pool_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(V)"));
+        const size_t tbytes = c->table.size() * sizeof(int32_t);
+        if ((e = hipMalloc(&c->d_table, tbytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(table)"));
+        if ((e = hipMemset(c->d_table, 0, tbytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(table)"));
+        if ((e = hipMalloc(&c->d_step, c->step_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(step)"));
+        if ((e = hipMalloc(&c->d_aux, c->aux_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(aux)"));
+        const size_t units = static_cast<size_t>(cfg->max_seqs) * c->ws_max_splits * cfg->num_heads;
+        if ((e = hipMalloc(&c->d_ws_acc, units * kva::kHeadDim * sizeof(float))) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMalloc(workspace)"));
+        if ((e = hipMalloc(&c->d_ws_ml, units * 2 * sizeof(float))) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMalloc(workspace ml)"));
+        const size_t cbytes = static_cast<size_t>(cfg->max_seqs) * cfg->num_kv_heads * sizeof(int32_t);
+        if ((e = hipMalloc(&c->d_counters, cbytes)) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMalloc(split counters)"));
+        if ((e = hipMemset(c->d_counters, 0, cbytes)) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMemset(split counters)"));
+        for (int i = 0; i < kStageSlots; ++i) {
+            if ((e = hipHostMalloc(reinterpret_cast<void **>(&c->h_stage[i]), c->stage_bytes,
+                                   hipHostMallocDefault)) != hipSuccess)
+                return cleanup(hip_fail(e, "hipHostMalloc(staging)"));
+            if ((e = hipEventCreateWithFlags(&c->ev[i], hipEventDisableTiming)) != hipSuccess)
+                return cleanup(hip_fail(e, "hipEventCreate"));
+        }
+        if ((e = hipDeviceSynchronize()) != hipSuccess) return cleanup(hip_fail(e, "hipDeviceSynchronize"));
+    }
+    *out = c;
+    return KVA_OK;
+}
+
+int kva_destroy(kva_cache *c) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (!c->host_only) {
+        (void)hipDeviceSynchronize();
+        for (int i = 0; i < kStageSlots; ++i) {
+            if (c->ev[i]) (void)hipEventDestroy(c->ev[i]);
+            if (c->h_stage[i]) (void)hipHostFree(c->h_stage[i]);
+        }
+        (void)hipFree(c->d_k);
+        (void)hipFree(c->d_v);
+        (void)hipFree(c->d_table);
+        (void)hipFree(c->d_step);
+        (void)hipFree(c->d_aux);
+        (void)hipFree(c->d_ws_acc);
+        (void)hipFree(c->d_ws_ml);
+        (void)hipFree(c->d_counters);
+    }
+    delete c;
+    return KVA_OK;
+}
+
+int kva_get_layout(const kva_cache *c, kva_layout *out) {
+    if (!c || !out) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    out->row_bytes = c->row_elems * sizeof(uint16_t);
+    out->block_bytes = out->row_bytes * kva::kBlockTokens;
+    out->layer_bytes = c->layer_elems * sizeof(uint16_t);
+    out->block_tokens = kva::kBlockTokens;
+    out->max_blocks_per_seq = c->cfg.max_blocks_per_seq;
+    return KVA_OK;
+}
+
+int kva_layer_pools(const kva_cache *c, int32_t layer, void **k_pool, void **v_pool) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (!k_pool || !v_pool) return fail(KVA_ERR_INVALID_ARG, "NULL output pointer");
+    *k_pool = c->d_k + c->layer_elems * layer;
+    *v_pool = c->d_v + c->layer_elems * layer;
+    return KVA_OK;
+}
+
+int kva_seq_reserve(kva_cache *c, int32_t seq, int32_t n_tokens) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_seq(c, seq);
+    if (rc) return rc;
+    if (n_tokens < 0) return fail(KVA_ERR_INVALID_ARG, "n_tokens %d < 0", n_tokens);
+    const int64_t need = (static_cast<int64_t>(n_tokens) + kva::kBlockTokens - 1) / kva::kBlockTokens;
+    if (need > c->cfg.max_blocks_per_seq)
+        return fail(KVA_ERR_CAPACITY, "sequence %d: %d tokens exceed capacity %d", seq, n_tokens,
+                    c->cfg.max_blocks_per_seq * kva::kBlockTokens);
+    return grow_seq(c, seq, static_cast<int32_t>(need));
+}
+
+int kva_seq_set_blocks(kva_cache *c, int32_t seq, const int32_t *ids, int32_t n) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_seq(c, seq);
+    if (rc) return rc;
+    if (n < 0 || (n > 0 && !ids)) return fail(KVA_ERR_INVALID_ARG, "bad block list");
+    if (n > c->cfg.max_blocks_per_seq)
+        return fail(KVA_ERR_CAPACITY, "%d blocks > max_blocks_per_seq %d", n, c->cfg.max_blocks_per_seq);
+    if (static_cast<int64_t>(n) * kva::kBlockTokens < c->len[seq])
+        return fail(KVA_ERR_CAPACITY, "%d blocks cannot hold the current length %d", n, c->len[seq]);
+    // Validate: in range, distinct, free (or already this sequence's).
+    const size_t base = static_cast<size_t>(seq) * c->cfg.max_blocks_per_seq;
+    std::vector<uint8_t> mine(c->cfg.max_blocks, 0), seen(c->cfg.max_blocks, 0);
+    for (int32_t i = 0; i < c->nblk[seq]; ++i) mine[c->table[base + i]] = 1;
+    for (int32_t i = 0; i < n; ++i) {
+        const int32_t b = ids[i];
+        if (b < 0 || b >= c->cfg.max_blocks)
+            return fail(KVA_ERR_BAD_BLOCK, "block id %d out of range [0, %d)", b, c->cfg.max_blocks);
+        if (seen[b]) return fail(KVA_ERR_BAD_BLOCK, "block id %d listed twice", b);
+        seen[b] = 1;
+        if (c->used[b] && !mine[b]) return fail(KVA_ERR_BAD_BLOCK, "block id %d is in use", b);
+    }
+    release_blocks(c, seq);
+    // Remove the new blocks from the free list.
+    c->free_list.erase(std::remove_if(c->free_list.begin(), c->free_list.end(),
+                                      [&](int32_t b) { return seen[b] != 0; }),
+                       c->free_list.end());
+    for (int32_t i = 0; i < n; ++i) {
+        c->used[ids[i]] = 1;
+        c->table[base + i] = ids[i];
+        c->patches.insert(c->patches.end(), {seq, i, ids[i]});
+    }
+    c->nblk[seq] = n;
+    c->freed[seq] = 0;
+    return KVA_OK;
+}
+
+int kva_seq_free(kva_cache *c, int32_t seq) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_seq(c, seq);
+    if (rc) return rc;
+    if (c->freed[seq]) return fail(KVA_ERR_DOUBLE_FREE, "sequence %d already freed", seq);
+    release_blocks(c, seq);
+    c->len[seq] = 0;
+    c->freed[seq] = 1;
+    c->step_valid = false;
+    return KVA_OK;
+}
+
+int kva_seq_get_len(const kva_cache *c, int32_t seq, int32_t *len) {
+    if (!c || !len) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    int rc = check_seq(c, seq);
+    if (rc) return rc;
+    *len = c->len[seq];
+    return KVA_OK;
+}
+
+int kva_seq_set_len(kva_cache *c, int32_t seq, int32_t len) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_seq(c, seq);
+    if (rc) return rc;
+    if (len < 0) return fail(KVA_ERR_ROLLBACK, "length %d < 0", len);
+    if (static_cast<int64_t>(len) > static_cast<int64_t>(c->nblk[seq]) * kva::kBlockTokens)
+        return fail(KVA_ERR_CAPACITY, "length %d exceeds reserved capacity %d", len,
+                    c->nblk[seq] * kva::kBlockTokens);
+    c->len[seq] = len;
+    c->step_valid = false;
+    return KVA_OK;
+}
+
+int kva_seq_get_blocks(const kva_cache *c, int32_t seq, int32_t *ids, int32_t cap, int32_t *n) {
+    if (!c || !n) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    int rc = check_seq(c, seq);
+    if (rc) return rc;
+    *n = c->nblk[seq];
+    if (ids) {
+        const size_t base = static_cast<size_t>(seq) * c->cfg.max_blocks_per_seq;
+        for (int32_t i = 0; i < std::min(cap, c->nblk[seq]); ++i) ids[i] = c->table[base + i];
+    }
+    return KVA_OK;
+}
+
+int kva_free_block_count(const kva_cache *c, int32_t *n) {
+    if (!c || !n) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    *n = static_cast<int32_t>(c->free_list.size());
+    return KVA_OK;
+}
+
+int kva_row_ptr(const kva_cache *c, int32_t layer, int32_t seq, int32_t slot, void **k_row,
+                void **v_row) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if ((rc = check_seq(c, seq))) return rc;
+    if (!k_row || !v_row) return fail(KVA_ERR_INVALID_ARG, "NULL output pointer");
+    if (slot < 0 || slot >= c->nblk[seq] * kva::kBlockTokens)
+        return fail(KVA_ERR_CAPACITY, "slot %d outside the %d reserved rows of sequence %d", slot,
+                    c->nblk[seq] * kva::kBlockTokens, seq);
+    const int32_t blk = c->table[static_cast<size_t>(seq) * c->cfg.max_blocks_per_seq + slot / kva::kBlockTokens];
+    const size_t off = c->layer_elems * layer +
+                       (static_cast<size_t>(blk) * kva::kBlockTokens + slot % kva::kBlockTokens) * c->row_elems;
+    *k_row = c->d_k + off;
+    *v_row = c->d_v + off;
+    return KVA_OK;
+}
+
+int kva_sync_tables(kva_cache *c, kva_stream_t stream) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    return flush_patches(c, static_cast<hipStream_t>(stream));
+}
+
+int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int32_t *n_new,
+                   const int32_t *rope_pos, const uint64_t *tree_bits, kva_stream_t stream) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    c->step_valid = false;
+    if (n_seqs <= 0 || n_seqs > c->cfg.max_seqs)
+        return fail(KVA_ERR_INVALID_ARG, "n_seqs %d outside [1, %d]", n_seqs, c->cfg.max_seqs);
+    if (!seq_ids || !n_new) return fail(KVA_ERR_INVALID_ARG, "seq_ids / n_new is NULL");
+    std::vector<uint8_t> seen(c->cfg.max_seqs, 0);
+    int64_t n_tok = 0;
+    int64_t extra_blocks = 0;
+    for (int32_t b = 0; b < n_seqs; ++b) {
+        const int32_t s = seq_ids[b];
+        int rc = check_seq(c, s);
+        if (rc) return rc;
+        if (seen[s]) return fail(KVA_ERR_INVALID_ARG, "sequence %d listed twice in one step", s);
+        seen[s] = 1;
+        if (n_new[b] < 0) return fail(KVA_ERR_INVALID_ARG, "n_new[%d] = %d < 0", b, n_new[b]);
+        const int64_t end = static_cast<int64_t>(c->len[s]) + n_new[b];
+        if (end > static_cast<int64_t>(c->cfg.max_blocks_per_seq) * kva::kBlockTokens)
+            return fail(KVA_ERR_CAPACITY, "sequence %d: length %lld exceeds capacity %d", s,
+                        static_cast<long long>(end), c->cfg.max_blocks_per_seq * kva::kBlockTokens);
+        const int64_t need = (end + kva::kBlockTokens - 1) / kva::kBlockTokens;
+        extra_blocks += std::max<int64_t>(0, need - c->nblk[s]);
+        n_tok += n_new[b];
+    }
+    if (n_tok > c->cfg.max_step_tokens)
+        return fail(KVA_ERR_CAPACITY, "step has %lld new tokens > max_step_tokens %d",
+                    static_cast<long long>(n_tok), c->cfg.max_step_tokens);
+    if (extra_blocks > static_cast<int64_t>(c->free_list.size()))
+        return fail(KVA_ERR_OUT_OF_BLOCKS, "step needs %lld more blocks, %zu free",
+                    static_cast<long long>(extra_blocks), c->free_list.size());
+    if (rope_pos)
+        for (int64_t i = 0; i < n_tok; ++i)
+            if (rope_pos[i] < 0) return fail(KVA_ERR_INVALID_ARG, "rope_pos[%lld] < 0", static_cast<long long>(i));
+    if (tree_bits) {
+        int64_t t = 0;
+        for (int32_t b = 0; b < n_seqs; ++b) {
+            if (n_new[b] > 64) return fail(KVA_ERR_UNSUPPORTED, "tree of %d nodes > 64", n_new[b]);
+            for (int32_t i = 0; i < n_new[b]; ++i, ++t) {
+                const uint64_t bits = tree_bits[t];
+                const uint64_t self = 1ull << i;
+                if (!(bits & self) || (bits >> i) != 1ull)
+                    return fail(KVA_ERR_INVALID_ARG,
+                                "tree_bits of node %d of sequence %d must contain itself and only earlier nodes",
+                                i, seq_ids[b]);
+            }
+        }
+    }
+    // Commit: reserve, assign slots, advance lengths.
+    for (int32_t b = 0; b < n_seqs; ++b) {
+        const int32_t s = seq_ids[b];
+        const int64_t end = static_cast<int64_t>(c->len[s]) + n_new[b];
+        int rc = grow_seq(c, s, static_cast<int32_t>((end + kva::kBlockTokens - 1) / kva::kBlockTokens));
+        if (rc) return rc;
+    }
+    const size_t o_seq = 0;
+    const size_t o_ctx = o_seq + sizeof(int32_t) * n_seqs;
+    const size_t o_start = o_ctx + sizeof(int32_t) * n_seqs;
+    const size_t o_tokoff = o_start + sizeof(int32_t) * n_seqs;
+    const size_t o_tseq = round_up(o_tokoff + sizeof(int32_t) * (n_seqs + 1), 16);
+    const size_t o_tslot = round_up(o_tseq + sizeof(int32_t) * n_tok, 16);
+    const size_t o_tpos = round_up(o_tslot + sizeof(int32_t) * n_tok, 16);
+    const size_t o_bits = round_up(o_tpos + sizeof(int32_t) * n_tok, 16);
+    const size_t total = o_bits + (tree_bits ? sizeof(uint64_t) * n_tok : 0);
+
+    std::vector<uint8_t> local;
+    uint8_t *h = nullptr;
+    int idx = -1;
+    if (c->host_only) {
+        local.resize(total + 16);
+        h = local.data();
+    } else {
+        int rc = acquire_stage(c, &h, &idx);
+        if (rc) return rc;
+    }
+    int32_t *p_seq = at<int32_t>(h, o_seq), *p_ctx = at<int32_t>(h, o_ctx),
+            *p_start = at<int32_t>(h, o_start), *p_off = at<int32_t>(h, o_tokoff),
+            *p_tseq = at<int32_t>(h, o_tseq), *p_tslot = at<int32_t>(h, o_tslot),
+            *p_tpos = at<int32_t>(h, o_tpos);
+    int32_t max_ctx = 0, max_new = 0, max_pos = 0;
+    int64_t sum_ctx = 0;
+    bool all_one = true;
+    int32_t t = 0;
+    for (int32_t b = 0; b < n_seqs; ++b) {
+        const int32_t s = seq_ids[b];
+        const int32_t start = c->len[s];
+        p_seq[b] = s;
+        p_start[b] = start;
+        p_ctx[b] = start + n_new[b];
+        p_off[b] = t;
+        for (int32_t i = 0; i < n_new[b]; ++i, ++t) {
+            p_tseq[t] = s;
+            p_tslot[t] = start + i;
+            p_tpos[t] = rope_pos ? rope_pos[t] : start + i;
+            max_pos = std::max(max_pos, p_tpos[t]);
+        }
+        c->len[s] = start + n_new[b];
+        max_ctx = std::max(max_ctx, p_ctx[b]);
+        max_new = std::max(max_new, n_new[b]);
+        sum_ctx += p_ctx[b];
+        all_one = all_one && n_new[b] == 1;
+    }
+    p_off[n_seqs] = t;
+    if (tree_bits) std::memcpy(h + o_bits, tree_bits, sizeof(uint64_t) * n_tok);
+
+    if (!c->host_only) {
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        KVA_HIP(hipMemcpyAsync(c->d_step, h, total, hipMemcpyHostToDevice, s));
+        int rc = release_stage(c, idx, s);
+        if (rc) return rc;
+        if ((rc = flush_patches(c, s))) return rc;
+    } else {
+        c->patches.clear();
+    }
+    c->off_seq = o_seq;
+    c->off_ctx = o_ctx;
+    c->off_start = o_start;
+    c->off_tokoff = o_tokoff;
+    c->off_tseq = o_tseq;
+    c->off_tslot = o_tslot;
+    c->off_tpos = o_tpos;
+    c->off_bits = o_bits;
+    c->st_n_seqs = n_seqs;
+    c->st_n_tok = static_cast<int32_t>(n_tok);
+    c->st_max_ctx = max_ctx;
+    c->st_max_new = max_new;
+    c->st_max_pos = max_pos;
+    c->st_sum_ctx = sum_ctx;
+    c->st_all_one = all_one;
+    c->st_has_bits = tree_bits != nullptr;
+    c->step_valid = true;
+    return KVA_OK;
+}
+
+int kva_append_qknorm_rope(kva_cache *c, int32_t layer, void *q, void *k, const void *v,
+                           const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                           const void *sin_tab, int32_t table_rows, kva_stream_t stream) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    if (c->st_n_tok == 0) return KVA_OK;
+    if (!q || !k || !v || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab)
+        return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(q_norm_w) || !aligned16(k_norm_w))
+        return fail(KVA_ERR_MISALIGNED, "q, k, v and norm weights must be 16-byte aligned");
+    const int half_rot = c->cfg.rotary_dim / 2;
+    if (half_rot > 0 && ((reinterpret_cast<uintptr_t>(cos_tab) | reinterpret_cast<uintptr_t>(sin_tab)) & 7u))
+        return fail(KVA_ERR_MISALIGNED, "cos/sin tables must be 8-byte aligned");
+    if (c->st_max_pos >= table_rows)
+        return fail(KVA_ERR_INVALID_ARG, "RoPE position %d beyond the %d table rows", c->st_max_pos,
+                    table_rows);
+    kva::AppendArgs a{};
+    a.q = static_cast<uint16_t *>(q);
+    a.k = static_cast<uint16_t *>(k);
+    a.v = static_cast<const uint16_t *>(v);
+    a.q_w = static_cast<const uint16_t *>(q_norm_w);
+    a.k_w = static_cast<const uint16_t *>(k_norm_w);
+    a.cos_tab = static_cast<const uint16_t *>(cos_tab);
+    a.sin_tab = static_cast<const uint16_t *>(sin_tab);
+    a.k_pool = c->d_k + c->layer_elems * layer;
+    a.v_pool = c->d_v + c->layer_elems * layer;
+    a.table = c->d_table;
+    a.table_stride = c->cfg.max_blocks_per_seq;
+    a.tok_seq = at<int32_t>(c->d_step, c->off_tseq);
+    a.tok_slot = at<int32_t>(c->d_step, c->off_tslot);
+    a.tok_pos = at<int32_t>(c->d_step, c->off_tpos);
+    a.n_tok = c->st_n_tok;
+    a.num_heads = c->cfg.num_heads;
+    a.num_kv_heads = c->cfg.num_kv_heads;
+    a.half_rot = half_rot;
+    a.eps = c->cfg.eps;
+    KVA_HIP(kva::launch_append(a, static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
+int kva_set_decode_split(kva_cache *c, int32_t split_tokens) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (split_tokens < 0 || split_tokens % kva::kSplitQuantum != 0)
+        return fail(KVA_ERR_INVALID_ARG, "split_tokens %d must be 0 or a positive multiple of %d",
+                    split_tokens, kva::kSplitQuantum);
+    c->split_user = split_tokens;
+    return KVA_OK;
+}
+
+int kva_get_decode_split(const kva_cache *c, int32_t *split_tokens, int32_t *n_splits) {
+    if (!c || !split_tokens || !n_splits) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    *split_tokens = c->last_split;
+    *n_splits = c->last_nsplits;
+    return KVA_OK;
+}
+
+int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    if (!c->st_all_one) return fail(KVA_ERR_STATE, "kva_decode needs exactly one new token per sequence");
+    if (!q || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
+    if (!aligned16(q) || !aligned16(out)) return fail(KVA_ERR_MISALIGNED, "q/out must be 16-byte aligned");
+    kva::DecodeArgs a{};
+    a.q = static_cast<const uint16_t *>(q);
+    a.k_pool = c->d_k + c->layer_elems * layer;
+    a.v_pool = c->d_v + c->layer_elems * layer;
+    a.table = c->d_table;
+    a.table_stride = c->cfg.max_blocks_per_seq;
+    a.seq_ids = at<int32_t>(c->d_step, c->off_seq);
+    a.ctx_lens = at<int32_t>(c->d_step, c->off_ctx);
+    a.n_seqs = c->st_n_seqs;
+    a.num_heads = c->cfg.num_heads;
+    a.num_kv_heads = c->cfg.num_kv_heads;
+    choose_split(c, c->st_max_ctx, c->st_sum_ctx, &a.split_tokens, &a.n_splits);
+    c->last_split = a.split_tokens;
+    c->last_nsplits = a.n_splits;
+    a.ws_acc = c->d_ws_acc;
+    a.ws_ml = c->d_ws_ml;
+    a.counters = c->d_counters;
+    a.out = static_cast<uint16_t *>(out);
+    KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
+static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream,
+                       bool tree) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    if (tree && !c->st_has_bits) return fail(KVA_ERR_STATE, "tree verify needs tree_bits in kva_step_begin");
+    if (!q || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
+    if (!aligned16(q) || !aligned16(out)) return fail(KVA_ERR_MISALIGNED, "q/out must be 16-byte aligned");
+    if (c->st_n_tok == 0) return KVA_OK;
+    kva::MultiQueryArgs a{};
+    a.q = static_cast<const uint16_t *>(q);
+    a.out = static_cast<uint16_t *>(out);
+    a.k_pool = c->d_k + c->layer_elems * layer;
+    a.v_pool = c->d_v + c->layer_elems * layer;
+    a.table = c->d_table;
+    a.table_stride = c->cfg.max_blocks_per_seq;
+    a.seq_ids = at<int32_t>(c->d_step, c->off_seq);
+    a.ctx_lens = at<int32_t>(c->d_step, c->off_ctx);
+    a.new_start = at<int32_t>(c->d_step, c->off_start);
+    a.tok_off = at<int32_t>(c->d_step, c->off_tokoff);
+    a.tok_bits = tree ? at<uint64_t>(c->d_step, c->off_bits) : nullptr;
+    a.n_seqs = c->st_n_seqs;
+    a.max_new = c->st_max_new;
+    a.num_heads = c->cfg.num_heads;
+    a.num_kv_heads = c->cfg.num_kv_heads;
+    a.tree = tree ? 1 : 0;
+    const hipError_t e = kva::launch_multi_query(a, static_cast<hipStream_t>(stream));
+    if (e == hipErrorNotSupported)
+        return fail(KVA_ERR_UNSUPPORTED, "multi-query attention kernel not available for this shape");
+    if (e != hipSuccess) return hip_fail(e, "launch_multi_query");
+    return KVA_OK;
+}
+
+int kva_prefill(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
+    return multi_query(c, layer, q, out, stream, false);
+}
+
+int kva_tree_verify(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
+    return multi_query(c, layer, q, out, stream, true);
+}
+
+int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int32_t *base_len,
+                 const int32_t *keep_off, const int32_t *keep_rows, kva_stream_t stream) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (n_seqs < 0 || n_seqs > c->cfg.max_seqs) return fail(KVA_ERR_INVALID_ARG, "bad n_seqs %d", n_seqs);
+    if (n_seqs == 0) return KVA_OK;
+    if (!seq_ids || !base_len || !keep_off) return fail(KVA_ERR_INVALID_ARG, "NULL index array");
+    if (keep_off[0] != 0) return fail(KVA_ERR_INVALID_ARG, "keep_off[0] must be 0");
+    std::vector<uint8_t> seen(c->cfg.max_seqs, 0);
+    std::vector<int32_t> moves;
+    std::vector<int32_t> move_off(1, 0);
+    for (int32_t b = 0; b < n_seqs; ++b) {
+        const int32_t s = seq_ids[b];
+        int rc = check_seq(c, s);
+        if (rc) return rc;
+        if (seen[s]) return fail(KVA_ERR_INVALID_ARG, "sequence %d listed twice", s);
+        seen[s] = 1;
+        const int32_t n = keep_off[b + 1] - keep_off[b];
+        if (n < 0) return fail(KVA_ERR_INVALID_ARG, "keep_off must be non-decreasing");
+        if (n > 0 && !keep_rows) return fail(KVA_ERR_INVALID_ARG, "keep_rows is NULL");
+        if (base_len[b] < 0 || base_len[b] > c->len[s])
+            return fail(KVA_ERR_ROLLBACK, "sequence %d: base length %d outside [0, %d]", s, base_len[b], c->len[s]);
+        int32_t prev = -1;
+        for (int32_t j = 0; j < n; ++j) {
+            const int32_t row = keep_rows[keep_off[b] + j];
+            if (row <= prev) return fail(KVA_ERR_ROLLBACK, "keep_rows of sequence %d not strictly increasing", s);
+            if (static_cast<int64_t>(base_len[b]) + row >= c->len[s])
+                return fail(KVA_ERR_ROLLBACK, "sequence %d: kept row %d beyond length %d", s,
+                            base_len[b] + row, c->len[s]);
+            prev = row;
+        }
+    }
+    for (int32_t b = 0; b < n_seqs; ++b) {
+        const int32_t s = seq_ids[b];
+        const int32_t n = keep_off[b + 1] - keep_off[b];
+        for (int32_t j = 0; j < n; ++j) {
+            const int32_t src = base_len[b] + keep_rows[keep_off[b] + j];
+            const int32_t dst = base_len[b] + j;
+            if (src != dst) moves.insert(moves.end(), {s, src, dst});
+        }
+        if (moves.size() / 3 > static_cast<size_t>(move_off.back())) move_off.push_back(static_cast<int32_t>(moves.size() / 3));
+        c->len[s] = base_len[b] + n;
+    }
+    c->step_valid = false;
+    const int32_t n_moves = static_cast<int32_t>(moves.size() / 3);
+    if (n_moves == 0 || c->host_only) return KVA_OK;
+    const int32_t n_groups = static_cast<int32_t>(move_off.size()) - 1;
+    const size_t bytes_moves = moves.size() * sizeof(int32_t);
+    const size_t o_off = round_up(bytes_moves, 16);
+    const size_t total = o_off + move_off.size() * sizeof(int32_t);
+    if (total > c->aux_bytes) return fail(KVA_ERR_CAPACITY, "rollback moves exceed the staging area");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint8_t *h;
+    int idx;
+    int rc = acquire_stage(c, &h, &idx);
+    if (rc) return rc;
+    std::memcpy(h, moves.data(), bytes_moves);
+    std::memcpy(h + o_off, move_off.data(), move_off.size() * sizeof(int32_t));
+    KVA_HIP(hipMemcpyAsync(c->d_aux, h, total, hipMemcpyHostToDevice, st));
+    if ((rc = release_stage(c, idx, st))) return rc;
+    kva::RollbackArgs a{};
+    a.k_pools = c->d_k;
+    a.v_pools = c->d_v;
+    a.layer_elems = c->layer_elems;
+    a.n_layers = c->cfg.n_layers;
+    a.table = c->d_table;
+    a.table_stride = c->cfg.max_blocks_per_seq;
+    a.moves = reinterpret_cast<const int32_t *>(c->d_aux);
+    a.move_off = reinterpret_cast<const int32_t *>(c->d_aux + o_off);
+    a.n_groups = n_groups;
+    a.num_kv_heads = c->cfg.num_kv_heads;
+    KVA_HIP(kva::launch_rollback(a, st));
+    return KVA_OK;
+}
+
+int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row, const void *sin_row,
+                           void *cache_dst, int32_t num_heads, int32_t head_dim, int32_t half_rotary,
+                           float eps, kva_stream_t stream) {
+    if (!x || !w) return fail(KVA_ERR_INVALID_ARG, "x / w is NULL");
+    if (num_heads < 0) return fail(KVA_ERR_INVALID_ARG, "num_heads %d < 0", num_heads);
+    if (!(head_dim == 64 || head_dim == 128 || head_dim == 256))
+        return fail(KVA_ERR_UNSUPPORTED, "head_dim %d unsupported (64, 128, 256)", head_dim);
+    if (half_rotary < 0 || half_rotary % 4 != 0 || 2 * half_rotary > head_dim)
+        return fail(KVA_ERR_UNSUPPORTED, "half_rotary %d must be a multiple of 4 with 2*half_rotary <= head_dim",
+                    half_rotary);
+    if (half_rotary > 0 && (!cos_row || !sin_row)) return fail(KVA_ERR_INVALID_ARG, "cos/sin row is NULL");
+    if (!aligned16(x) || !aligned16(w) || (cache_dst && !aligned16(cache_dst)))
+        return fail(KVA_ERR_MISALIGNED, "x, w and cache_dst must be 16-byte aligned");
+    if (half_rotary > 0 && ((reinterpret_cast<uintptr_t>(cos_row) | reinterpret_cast<uintptr_t>(sin_row)) & 7u))
+        return fail(KVA_ERR_MISALIGNED, "cos/sin rows must be 8-byte aligned");
+    if (!(eps >= 0.0f)) return fail(KVA_ERR_INVALID_ARG, "eps must be >= 0");
+    kva::LegacyNormArgs a{};
+    a.x = static_cast<uint16_t *>(x);
+    a.w = static_cast<const uint16_t *>(w);
+    a.cos_row = static_cast<const uint16_t *>(cos_row);
+    a.sin_row = static_cast<const uint16_t *>(sin_row);
+    a.cache_dst = static_cast<uint16_t *>(cache_dst);
+    a.num_heads = num_heads;
+    a.head_dim = head_dim;
+    a.half_rot = half_rotary;
+    a.eps = eps;
+    KVA_HIP(kva::launch_legacy_norm(a, static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
+static int legacy_decode(kva_cache *ws, const void *q, const void *k_base, const void *v_base,
+                         void *out, int32_t kv_seq_len, int32_t batch, int64_t batch_stride,
+                         int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream) {
+    if (!q || !k_base || !v_base || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
+    if (kv_seq_len <= 0) return fail(KVA_ERR_INVALID_ARG, "kv_seq_len %d must be positive", kv_seq_len);
+    if (batch <= 0 || batch > 65535) return fail(KVA_ERR_INVALID_ARG, "batch %d outside [1, 65535]", batch);
+    if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+        return fail(KVA_ERR_INVALID_ARG, "num_heads %d must be a positive multiple of num_kv_heads %d",
+                    num_heads, num_kv_heads);
+    const int g = num_heads / num_kv_heads;
+    if (!(g == 1 || g == 2 || g == 3 || g == 4 || g == 6 || g == 8))
+        return fail(KVA_ERR_UNSUPPORTED, "GQA group %d unsupported", g);
+    if (!aligned16(q) || !aligned16(k_base) || !aligned16(v_base) || !aligned16(out))
+        return fail(KVA_ERR_MISALIGNED, "q, K, V and out must be 16-byte aligned");
+    const int64_t row_bytes = static_cast<int64_t>(num_kv_heads) * kva::kHeadDim * 2;
+    if (batch > 1 && (batch_stride % 16 != 0 || batch_stride < row_bytes * kv_seq_len))
+        return fail(KVA_ERR_INVALID_ARG, "batch_stride %lld must be a multiple of 16 covering %d rows",
+                    static_cast<long long>(batch_stride), kv_seq_len);
+    if (ws && ws->host_only) return fail(KVA_ERR_NO_DEVICE, "workspace cache is host-only");
+    kva::DecodeArgs a{};
+    a.q = static_cast<const uint16_t *>(q);
+    a.k_pool = static_cast<const uint16_t *>(k_base);
+    a.v_pool = static_cast<const uint16_t *>(v_base);
+    a.seq_stride = static_cast<size_t>(batch_stride / 2);
+    a.ctx_len_const = kv_seq_len;
+    a.n_seqs = batch;
+    a.num_heads = num_heads;
+    a.num_kv_heads = num_kv_heads;
+    a.split_tokens = (kv_seq_len + kva::kSplitQuantum - 1) / kva::kSplitQuantum * kva::kSplitQuantum;
+    a.n_splits = 1;
+    if (ws) {
+        int32_t split, ns;
+        choose_split(ws, kv_seq_len, static_cast<int64_t>(kv_seq_len) * batch, &split, &ns);
+        // The workspace holds max_seqs * ws_max_splits * cfg.num_heads partial rows.
+        if (ns > 1 &&
+            static_cast<int64_t>(ns) * num_heads * batch <=
+                static_cast<int64_t>(ws->ws_max_splits) * ws->cfg.num_heads * ws->cfg.max_seqs &&
+            static_cast<int64_t>(batch) * num_kv_heads <=
+                static_cast<int64_t>(ws->cfg.max_seqs) * ws->cfg.num_kv_heads) {
+            a.split_tokens = split;
+            a.n_splits = ns;
+            a.ws_acc = ws->d_ws_acc;
+            a.ws_ml = ws->d_ws_ml;
+            a.counters = ws->d_counters;
+        }
+    }
+    a.out = static_cast<uint16_t *>(out);
+    KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
+int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base, const void *v_base,
+                      void *out, int32_t kv_seq_len, int32_t num_heads, int32_t num_kv_heads,
+                      kva_stream_t stream) {
+    return legacy_decode(ws, q, k_base, v_base, out, kv_seq_len, 1, 0, num_heads, num_kv_heads, stream);
+}
+
+int kva_legacy_decode_batched(kva_cache *ws, const void *q, const void *k_base, const void *v_base,
+                              void *out, int32_t kv_seq_len, int32_t batch, int64_t batch_stride,
+                              int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream) {
+    return legacy_decode(ws, q, k_base, v_base, out, kv_seq_len, batch, batch_stride, num_heads,
+                         num_kv_heads, stream);
+}
+
+int kva_hbm_copy(void *dst, const void *src, size_t bytes, kva_stream_t stream) {
+    if (!dst || !src) return fail(KVA_ERR_INVALID_ARG, "NULL pointer");
+    if (bytes % 16 != 0) return fail(KVA_ERR_INVALID_ARG, "bytes %zu not a multiple of 16", bytes);
+    if (!aligned16(dst) || !aligned16(src)) return fail(KVA_ERR_MISALIGNED, "pointers must be 16-byte aligned");
+    KVA_HIP(kva::launch_copy(dst, src, bytes, static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
+// ---- device helpers -------------------------------------------------------
+int kva_dev_count(int32_t *n) {
+    if (!n) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    int c = 0;
+    KVA_HIP(hipGetDeviceCount(&c));
+    *n = c;
+    return KVA_OK;
+}
+int kva_dev_set(int32_t d) {
+    KVA_HIP(hipSetDevice(d));
+    return KVA_OK;
+}
+int kva_dev_malloc(void **p, size_t n) {
+    if (!p) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    KVA_HIP(hipMalloc(p, n));
+    return KVA_OK;
+}
+int kva_dev_free(void *p) {
+    KVA_HIP(hipFree(p));
+    return KVA_OK;
+}
+int kva_memcpy_h2d(void *d, const void *s, size_t n) {
+    KVA_HIP(hipMemcpy(d, s, n, hipMemcpyHostToDevice));
+    return KVA_OK;
+}
+int kva_memcpy_d2h(void *d, const void *s, size_t n) {
+    KVA_HIP(hipMemcpy(d, s, n, hipMemcpyDeviceToHost));
+    return KVA_OK;
+}
+int kva_memcpy_d2d(void *d, const void *s, size_t n) {
+    KVA_HIP(hipMemcpy(d, s, n, hipMemcpyDeviceToDevice));
+    return KVA_OK;
+}
+int kva_memset(void *d, int32_t v, size_t n) {
+    KVA_HIP(hipMemset(d, v, n));
+    return KVA_OK;
+}
+int kva_dev_synchronize(void) {
+    KVA_HIP(hipDeviceSynchronize());
+    return KVA_OK;
+}
+int kva_stream_create(kva_stream_t *s) {
+    if (!s) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    hipStream_t st;
+    KVA_HIP(hipStreamCreate(&st));
+    *s = st;
+    return KVA_OK;
+}
+int kva_stream_destroy(kva_stream_t s) {
+    KVA_HIP(hipStreamDestroy(static_cast<hipStream_t>(s)));
+    return KVA_OK;
+}
+int kva_stream_synchronize(kva_stream_t s) {
+    KVA_HIP(hipStreamSynchronize(static_cast<hipStream_t>(s)));
+    return KVA_OK;
+}
+int kva_event_create(kva_event_t *ev) {
+    if (!ev) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    hipEvent_t e;
+    KVA_HIP(hipEventCreate(&e));
+    *ev = e;
+    return KVA_OK;
+}
+int kva_event_destroy(kva_event_t ev) {
+    KVA_HIP(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+    return KVA_OK;
+}
+int kva_event_record(kva_event_t ev, kva_stream_t s) {
+    KVA_HIP(hipEventRecord(static_cast<hipEvent_t>(ev), static_cast<hipStream_t>(s)));
+    return KVA_OK;
+}
+int kva_event_synchronize(kva_event_t ev) {
+    KVA_HIP(hipEventSynchronize(static_cast<hipEvent_t>(ev)));
+    return KVA_OK;
+}
+int kva_event_elapsed_ms(float *ms, kva_event_t a, kva_event_t b) {
+    if (!ms) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    KVA_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)));
+    return KVA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+// Internal interface between the host side of libkvattn (kva_host.cpp, built
+// with g++) and the HIP kernels (k_*.hip, built with hipcc for gfx950).
+// Only plain types cross this boundary: fp16 tensors are uint16_t pointers.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace kva {
+
+constexpr int kHeadDim = 256;     // the only head_dim the paged kernels take
+constexpr int kBlockTokens = 16;  // tokens per page
+constexpr int kDecodeWaves = 4;   // waves per decode workgroup
+constexpr int kSplitQuantum = 64; // decode split sizes are multiples of this
+
+// Fused QK-RMSNorm + RoPE + K/V append over all new tokens of a step.
+struct AppendArgs {
+    uint16_t *q;              // [T][H][256], normalised + rotated in place
+    uint16_t *k;              // [T][Hkv][256], normalised + rotated in place
+    const uint16_t *v;        // [T][Hkv][256]
+    const uint16_t *q_w;      // [256]
+    const uint16_t *k_w;      // [256]
+    const uint16_t *cos_tab;  // [rows][half_rot]
+    const uint16_t *sin_tab;
+    uint16_t *k_pool;         // this layer's pool [blocks][16][Hkv][256]
+    uint16_t *v_pool;
+    const int32_t *table;     // [max_seqs][table_stride]
+    int32_t table_stride;
+    const int32_t *tok_seq;   // device: sequence id of each new token
+    const int32_t *tok_slot;  // device: logical slot of each new token
+    const int32_t *tok_pos;   // device: RoPE position of each new token
+    int32_t n_tok;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t half_rot;
+    float eps;
+};
+hipError_t launch_append(const AppendArgs &a, hipStream_t s);
+
+// Reference-compatible norm+RoPE on a contiguous [n_heads][head_dim] buffer.
+struct LegacyNormArgs {
+    uint16_t *x;
+    const uint16_t *w;
+    const uint16_t *cos_row;
+    const uint16_t *sin_row;
+    uint16_t *cache_dst;      // nullable
+    int32_t num_heads;
+    int32_t head_dim;         // 64, 128 or 256
+    int32_t half_rot;
+    float eps;
+};
+hipError_t launch_legacy_norm(const LegacyNormArgs &a, hipStream_t s);
+
+// Split-K GQA decode over a paged (or contiguous) cache.
+struct DecodeArgs {
+    const uint16_t *q;        // [n_seqs][H][256]
+    const uint16_t *k_pool;   // layer base (or contiguous K when table == null)
+    const uint16_t *v_pool;
+    const int32_t *table;     // device block table, null = contiguous cache
+    int32_t table_stride;
+    size_t seq_stride;        // contiguous cache: elements between sequences
+    const int32_t *seq_ids;   // device [n_seqs] (ignored when table == null)
+    const int32_t *ctx_lens;  // device [n_seqs] (null: use ctx_len_const)
+    int32_t ctx_len_const;
+    int32_t n_seqs;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t split_tokens;     // multiple of kSplitQuantum
+    int32_t n_splits;         // grid.x; 1 = outputs written directly
+    float *ws_acc;            // [n_seqs][n_splits][Hkv][G][256] (split mode)
+    float *ws_ml;             // [n_seqs][n_splits][Hkv][G][2]
+    int32_t *counters;        // [n_seqs][Hkv] split arrivals, zero between launches
+    uint16_t *out;            // [n_seqs][H][256]
+};
+hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
+
+// Apply block-table patches (seq, index, block) staged by a step.
+hipError_t launch_table_patch(int32_t *table, int32_t table_stride,
+                              const int32_t *patches, int32_t n_patches,
+                              hipStream_t s);
+
+// Streaming device copy (bytes multiple of 16): the HBM bandwidth probe.
+hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
+
+// Move accepted rows of each sequence, in every layer (tree rollback).
+struct RollbackArgs {
+    uint16_t *k_pools;        // base of layer 0; layers are layer_elems apart
+    uint16_t *v_pools;
+    size_t layer_elems;
+    int32_t n_layers;
+    const int32_t *table;
+    int32_t table_stride;
+    const int32_t *moves;     // device [n_moves][3]: seq, src slot, dst slot
+    const int32_t *move_off;  // device [n_groups+1]: moves of one sequence
+    int32_t n_groups;
+    int32_t num_kv_heads;
+};
+hipError_t launch_rollback(const RollbackArgs &a, hipStream_t s);
+
+// Multi-query (prefill / tree) attention with MFMA tiles.
+struct MultiQueryArgs {
+    const uint16_t *q;        // [T][H][256]
+    uint16_t *out;            // [T][H][256]
+    const uint16_t *k_pool;
+    const uint16_t *v_pool;
+    const int32_t *table;
+    int32_t table_stride;
+    const int32_t *seq_ids;   // device [n_seqs]
+    const int32_t *ctx_lens;  // device [n_seqs]: length after the step
+    const int32_t *new_start; // device [n_seqs]: first new slot
+    const int32_t *tok_off;   // device [n_seqs+1]: new-token ranges
+    const uint64_t *tok_bits; // device [T] (tree mode) or null
+    int32_t n_seqs;
+    int32_t max_new;          // most new tokens of one sequence
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t tree;             // 0 = causal chunk, 1 = tree mask
+};
+hipError_t launch_multi_query(const MultiQueryArgs &a, hipStream_t s);
+
+}  // namespace kva

@@ -1,0 +1,171 @@
+"""GPU parity: split-K GQA decode against the FP32 oracle (tolerance 2e-3).
+
+Covers config 1 against its golden fixture, ragged batches through permuted
+block tables with lengths at page and split edges, every split size path
+(single split = direct output, many splits + combine), exact special cases,
+the reference's own decode regression shapes through the contiguous entry
+point (tests/test_flash_attn_v3.py:281-312, where its bar was 1e-2), and
+the full config-3 workload (32 sequences, lengths U[1024, 8192], seed 0).
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from mi50grad_amd import _lib
+from mi50grad_amd.workloads import c3_spec
+from oracle import kvattn_oracle as orc
+
+from gpu_helpers import HKV, H, D, Tables, build_cache, expected_norm, max_err, say
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def run_decode_step(device, cache, k_rows, v_rows, lengths, rng, tables, split=0, layer=0):
+    """Append one token per sequence, decode, return (gpu out, oracle out)."""
+    B = len(lengths)
+    q = rng.standard_normal((B, H, D), dtype=np.float32).astype(np.float16)
+    k = rng.standard_normal((B, HKV, D), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((B, HKV, D), dtype=np.float32).astype(np.float16)
+    qw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    kw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    dq, dk, dv, out = device.array(q), device.array(k), device.array(v), device.empty((B, H, D), np.float16)
+    cache.set_decode_split(split)
+    cache.begin_step(list(range(B)), [1] * B)
+    cache.append(layer, dq, dk, dv, device.array(qw), device.array(kw), tables.d_cos, tables.d_sin,
+                 tables.rows)
+    cache.decode(layer, dq, out)
+    device.synchronize()
+    pos = np.asarray(lengths)
+    qn = expected_norm(q, qw, tables, pos)
+    kn = expected_norm(k, kw, tables, pos)
+    ks = [np.concatenate([k_rows[layer][b], kn[b:b + 1]]) for b in range(B)]
+    vs = [np.concatenate([v_rows[layer][b], v[b:b + 1]]) for b in range(B)]
+    return out.numpy(), orc.decode_attention(qn, ks, vs), qn, ks, vs
+
+
+def test_decode_c1_golden(device):
+    fx = np.load(Path(__file__).resolve().parent / "golden" / "c1_golden.npz")
+    say("decode c1 golden")
+    cache, _, _ = build_cache([0], [list(range(16))], extra_rows=256, fill=False)
+    # Cache rows 0..254 from the fixture, written through the row pointers.
+    for s in range(255):
+        kp, vp = cache.row_ptr(0, 0, s)
+        _lib.call("kva_memcpy_h2d", kp, np.ascontiguousarray(fx["k_cache"][s]).ctypes.data, HKV * D * 2)
+        _lib.call("kva_memcpy_h2d", vp, np.ascontiguousarray(fx["v_cache"][s]).ctypes.data, HKV * D * 2)
+    cache.set_len(0, 255)
+    tables = Tables(device, 256)
+    dq = device.array(fx["q"])
+    out = device.empty((1, H, D), np.float16)
+    cache.begin_step([0], [1])
+    cache.append(0, dq, device.array(fx["k_new"]), device.array(fx["v_new"]),
+                 device.array(fx["q_norm"]), device.array(fx["k_norm"]), tables.d_cos, tables.d_sin, 256)
+    cache.decode(0, dq, out)
+    device.synchronize()
+    assert max_err(out.numpy()[0], fx["out_fp32"]) <= TOL
+    cache.destroy()
+
+
+@pytest.mark.parametrize("split", [0, 64, 128, 1024, 8192])
+def test_decode_ragged_permuted(device, split):
+    rng = np.random.default_rng(100 + split)
+    lengths = [0, 1, 14, 15, 16, 62, 63, 64, 127, 128, 500, 1000, 2047, 4097]
+    nblk = [(L + 1 + 15) // 16 for L in lengths]
+    perm = rng.permutation(sum(nblk))
+    ids, o = [], 0
+    for n in nblk:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say(f"decode ragged split={split}")
+    cache, kr, vr = build_cache(lengths, ids, extra_rows=1, rng=rng)
+    tables = Tables(device, 8192)
+    got, exp, *_ = run_decode_step(device, cache, kr, vr, lengths, rng, tables, split=split)
+    err = max_err(got, exp)
+    assert err <= TOL, (err, cache.decode_split())
+    cache.destroy()
+
+
+def test_decode_special_cases(device):
+    rng = np.random.default_rng(9)
+    say("decode special cases")
+    cache, kr, vr = build_cache([0, 40, 40], [[0], [1, 2, 3], [4, 5, 6]], extra_rows=1, rng=rng)
+    # Sequence 1: all cached keys equal to the (normed) appended key is hard
+    # to arrange through the norm, so use identical cached V instead: the
+    # output must equal that V row whatever the weights are.
+    vconst = rng.standard_normal((1, HKV, D), dtype=np.float32).astype(np.float16)
+    tables = Tables(device, 64)
+    B = 3
+    q = rng.standard_normal((B, H, D), dtype=np.float32).astype(np.float16)
+    k = rng.standard_normal((B, HKV, D), dtype=np.float32).astype(np.float16)
+    v = np.repeat(vconst, B, 0)
+    for s in range(40):
+        for b in (1,):
+            _, vp = cache.row_ptr(0, b, s)
+            _lib.call("kva_memcpy_h2d", vp, np.ascontiguousarray(vconst[0]).ctypes.data, HKV * D * 2)
+    ones = np.ones(D, np.float16)
+    dq = device.array(q)
+    out = device.empty((B, H, D), np.float16)
+    cache.begin_step([0, 1, 2], [1, 1, 1])
+    cache.append(0, dq, device.array(k), device.array(v), device.array(ones), device.array(ones),
+                 tables.d_cos, tables.d_sin, tables.rows)
+    cache.decode(0, dq, out)
+    device.synchronize()
+    o = out.numpy()
+    # L = 1 (sequence 0): the output is the appended V row, exactly.
+    assert np.array_equal(o[0].view(np.uint16), np.repeat(vconst[0], 6, 0).view(np.uint16))
+    # All V rows equal (sequence 1): the output is that row within fp16 rounding.
+    assert max_err(o[1], np.repeat(vconst[0], 6, 0)) <= 1e-3
+    cache.destroy()
+
+
+@pytest.mark.parametrize("h,hkv,L", [(4, 2, 256), (4, 4, 256), (8, 2, 512), (48, 8, 256),
+                                     (48, 8, 512), (48, 8, 1024), (24, 4, 255), (24, 4, 17)])
+def test_legacy_decode_reference_shapes(device, h, hkv, L):
+    """tests/test_flash_attn_v3.py:281-312 (seed 7, x0.1 inputs); contiguous
+    K/V of exactly L rows, so the last partial page must not read past them."""
+    np.random.seed(7)
+    Q = (np.random.randn(1, h, 256) * 0.1).astype(np.float16)
+    K = (np.random.randn(L, hkv, 256) * 0.1).astype(np.float16)
+    V = (np.random.randn(L, hkv, 256) * 0.1).astype(np.float16)
+    say(f"legacy decode h={h} hkv={hkv} L={L}")
+    dq, dk, dv = device.array(Q), device.array(K), device.array(V)
+    out = device.empty((1, h, 256), np.float16)
+    _lib.call("kva_legacy_decode", None, dq.ptr, dk.ptr, dv.ptr, out.ptr, L, h, hkv, None)
+    device.synchronize()
+    ref = orc.attention_fp32(Q, K, V)
+    assert max_err(out.numpy(), ref) <= TOL
+
+
+def test_legacy_decode_batched_and_workspace(device):
+    rng = np.random.default_rng(12)
+    B, L, stride_rows = 3, 700, 768
+    K = rng.standard_normal((B, stride_rows, HKV, D), dtype=np.float32).astype(np.float16)
+    V = rng.standard_normal((B, stride_rows, HKV, D), dtype=np.float32).astype(np.float16)
+    Q = rng.standard_normal((B, H, D), dtype=np.float32).astype(np.float16)
+    say("legacy decode batched")
+    ws_cache, _, _ = build_cache([0], [[0]], extra_rows=1, fill=False)
+    ws_cache.set_decode_split(128)
+    dq, dk, dv = device.array(Q), device.array(K), device.array(V)
+    out = device.empty((B, H, D), np.float16)
+    _lib.call("kva_legacy_decode_batched", ws_cache.handle, dq.ptr, dk.ptr, dv.ptr, out.ptr, L, B,
+              stride_rows * HKV * D * 2, H, HKV, None)
+    device.synchronize()
+    ref = np.stack([orc.attention_fp32(Q[b:b + 1], K[b, :L], V[b, :L])[0] for b in range(B)])
+    assert max_err(out.numpy(), ref) <= TOL
+    ws_cache.destroy()
+
+
+def test_decode_c3_full_workload(device):
+    """Config 3 exactly: B=32, lengths U[1024, 8192] (seed 0), permuted pages."""
+    spec = c3_spec(0)
+    rng = np.random.default_rng(1)
+    say("decode c3 full workload")
+    cache, kr, vr = build_cache(list(spec.lengths), spec.block_ids, extra_rows=1, rng=rng)
+    tables = Tables(device, 8193)
+    got, exp, *_ = run_decode_step(device, cache, kr, vr, list(spec.lengths), rng, tables)
+    err = max_err(got, exp)
+    split, ns = cache.decode_split()
+    print(f"c3 max err {err:.2e} split {split} x {ns}")
+    assert err <= TOL
+    cache.destroy()

@@ -1,0 +1,171 @@
+"""Host-side bookkeeping of libkvattn on a host-only cache (CPU only).
+
+Covers the failure handling the C ABI validates before any launch: bad
+arguments, capacity and pool exhaustion, double free, rollback past the
+base, unsorted keep lists, call order.  No device memory is touched.
+"""
+import pytest
+
+from mi50grad_amd._lib import KvaError
+from mi50grad_amd.kv_cache import PagedKVCache
+
+
+def make(**kw):
+    args = dict(n_layers=2, max_seqs=4, max_blocks=20, max_blocks_per_seq=8, max_step_tokens=64,
+                host_only=True)
+    args.update(kw)
+    return PagedKVCache(**args)
+
+
+def code(excinfo):
+    return excinfo.value.code
+
+
+def test_config_validation():
+    with pytest.raises(KvaError) as e:
+        make(n_layers=0)
+    assert code(e) == -1
+    for bad in (dict(num_heads=24, num_kv_heads=5), dict(num_heads=20, num_kv_heads=4)):
+        with pytest.raises(KvaError):
+            make(**bad)
+    with pytest.raises(KvaError) as e:
+        make(head_dim=128)
+    assert code(e) == -2
+
+
+def test_reserve_grows_a_page_at_a_time():
+    c = make()
+    assert c.free_block_count() == 20
+    c.reserve(0, 1)
+    assert len(c.blocks(0)) == 1
+    c.reserve(0, 16)
+    assert len(c.blocks(0)) == 1
+    c.reserve(0, 17)
+    assert len(c.blocks(0)) == 2
+    assert c.free_block_count() == 18
+    with pytest.raises(KvaError) as e:
+        c.reserve(0, 8 * 16 + 1)
+    assert code(e) == -5
+
+
+def test_pool_exhaustion_and_free():
+    c = make(max_blocks=5)
+    c.reserve(0, 64)
+    with pytest.raises(KvaError) as e:
+        c.reserve(1, 32)
+    assert code(e) == -4
+    c.free_seq(0)
+    assert c.free_block_count() == 5
+    with pytest.raises(KvaError) as e:
+        c.free_seq(0)
+    assert code(e) == -11
+    c.reserve(1, 32)
+    assert len(c.blocks(1)) == 2
+
+
+def test_set_blocks_validation():
+    c = make()
+    c.set_blocks(0, [7, 3, 11])
+    assert c.blocks(0) == [7, 3, 11]
+    with pytest.raises(KvaError) as e:
+        c.set_blocks(1, [3])                  # in use by sequence 0
+    assert code(e) == -7
+    with pytest.raises(KvaError) as e:
+        c.set_blocks(1, [99])                 # out of range
+    assert code(e) == -7
+    with pytest.raises(KvaError) as e:
+        c.set_blocks(1, [4, 4])               # duplicate
+    assert code(e) == -7
+    c.set_blocks(0, [3, 12])                  # re-plan: keeps 3, releases 7 and 11
+    assert c.free_block_count() == 18
+
+
+def test_bad_sequence_ids():
+    c = make()
+    for s in (-1, 4):
+        with pytest.raises(KvaError) as e:
+            c.reserve(s, 1)
+        assert code(e) == -6
+
+
+def test_step_assigns_slots_and_lengths():
+    c = make()
+    c.begin_step([0, 2], [1, 5])
+    assert c.seq_len(0) == 1 and c.seq_len(2) == 5
+    c.begin_step([2], [12])
+    assert c.seq_len(2) == 17 and len(c.blocks(2)) == 2
+    with pytest.raises(KvaError) as e:
+        c.begin_step([0, 0], [1, 1])          # a sequence twice
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        c.begin_step([1], [65])               # beyond max_step_tokens
+    assert code(e) == -5
+    with pytest.raises(KvaError) as e:
+        c.begin_step([1], [-1])
+    assert code(e) == -1
+
+
+def test_step_capacity_checked_before_commit():
+    c = make(max_blocks=3)
+    c.begin_step([0], [16])
+    with pytest.raises(KvaError) as e:
+        c.begin_step([0, 1], [16, 32])        # needs 3 more blocks, 2 free
+    assert code(e) == -4
+    assert c.seq_len(0) == 16 and c.seq_len(1) == 0   # nothing committed
+
+
+def test_tree_bits_validation():
+    c = make()
+    with pytest.raises(KvaError):
+        c.begin_step([0], [3], tree_bits=[0b001, 0b001, 0b101])   # node 1 misses itself
+    c2 = make()
+    with pytest.raises(KvaError):
+        c2.begin_step([0], [2], tree_bits=[0b11, 0b10])            # root sees a later node
+    assert c.seq_len(0) == 0 and c2.seq_len(0) == 0
+    c3 = make()
+    c3.begin_step([0], [3], tree_bits=[0b001, 0b011, 0b101], rope_pos=[0, 1, 1])
+    assert c3.seq_len(0) == 3
+
+
+def test_hot_calls_need_a_device_and_a_step():
+    c = make()
+    with pytest.raises(KvaError) as e:
+        c.decode(0, 1 << 20, 1 << 20)
+    assert code(e) == -3
+
+
+def test_rollback_validation_and_lengths():
+    c = make()
+    c.begin_step([0, 1], [20, 9])
+    c.rollback([0, 1], [11, 0], [[0, 2, 3], []])
+    assert c.seq_len(0) == 14 and c.seq_len(1) == 0
+    c.begin_step([0], [9])                    # length 23
+    with pytest.raises(KvaError) as e:
+        c.rollback([0], [14], [[2, 1]])       # not increasing
+    assert code(e) == -9
+    with pytest.raises(KvaError) as e:
+        c.rollback([0], [14], [[0, 9]])       # beyond the length
+    assert code(e) == -9
+    with pytest.raises(KvaError) as e:
+        c.rollback([0], [24], [[]])           # base past the length
+    assert code(e) == -9
+    assert c.seq_len(0) == 23
+
+
+def test_set_len_bounds():
+    c = make()
+    c.reserve(0, 20)
+    c.set_len(0, 32)
+    with pytest.raises(KvaError) as e:
+        c.set_len(0, 33)
+    assert code(e) == -5
+    with pytest.raises(KvaError) as e:
+        c.set_len(0, -1)
+    assert code(e) == -9
+
+
+def test_decode_split_setting():
+    c = make()
+    c.set_decode_split(128)
+    with pytest.raises(KvaError):
+        c.set_decode_split(100)
