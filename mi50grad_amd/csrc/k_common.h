@@ -37,11 +37,20 @@ enum : int {
     kDppQuadXor2 = 0x4E,       // quad_perm [2,3,0,1]
     kDppRowHalfMirror = 0x141, // lane i <-> 7-i inside each 8 lanes
     kDppRowRor8 = 0x128,       // rotate a 16-lane row by 8
+    kDppRowMirror = 0x140,     // lane i <-> 15-i inside each row
+    kDppRowBcast15 = 0x142,    // lane 15 of a row -> all lanes of the next row
+    kDppRowBcast31 = 0x143,    // lane 31 -> all lanes of rows 2 and 3
 };
 template <int Ctrl>
 __device__ __forceinline__ float dpp_f(float x) {
     return __builtin_bit_cast(
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), Ctrl, 0xF, 0xF, false));
+}
+// DPP move restricted to the rows in RowMask; other rows keep x.
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ float dpp_masked_f(float x) {
+    const int xi = __builtin_bit_cast(int, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(xi, xi, Ctrl, RowMask, 0xF, false));
 }
 
 // Sum over the 8 lanes of an aligned 8-lane group; every lane gets the sum.

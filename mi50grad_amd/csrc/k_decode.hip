@@ -5,22 +5,27 @@
 // (:222) — generalised to a batch of sequences with ragged lengths read
 // through a block table, and to any number of KV splits.
 //
-// Work unit: one 256-thread workgroup per (split, kv head, sequence).  The
-// G = H/Hkv query heads of the KV head share every K/V byte the workgroup
-// loads (the reference re-read each KV head G times, once per query head).
-// The four waves take interleaved 16-token pages of the split, each with its
-// own online-softmax state, and merge through LDS at the end.
+// Work split: stream-K over pages (see decode_kernel).  A 256-thread
+// workgroup processes (sequence, kv head) unit segments; the G = H/Hkv query
+// heads of the KV head share every K/V byte it loads (the reference re-read
+// each KV head G times, once per query head).  The four waves take
+// interleaved 16-token pages of a segment, each with its own online-softmax
+// state, and merge through LDS at the segment's end.
 //
-// Per page, per wave (lane = 8*r + j):
-//   QK: lanes of group r hold tokens r and r+8, 32 dims each (pieces
-//       j, j+8, j+16, j+24 of 16 bytes), dot with the G query heads via
-//       v_dot2_f32_f16; an 8-lane DPP sum finishes each score.
-//   softmax: scores in the log2 domain; page max across the 8 groups with
-//       DPP row rotate + two cross-row shuffles; v_exp_f32.
-//   PV: lane owns dims 4*lane..4*lane+3 of all G heads; tokens r and r+8
+// Per page, per wave (lane = 16*r + j):
+//   loads: the next page's K is prefetched into the second of two register
+//       buffers (ping-pong) and the current page's V is issued before QK, so
+//       every wave keeps 8-16 KB in flight during its arithmetic;
+//   QK: the 16 lanes of row r hold tokens r, r+4, r+8, r+12, 16 dims each
+//       (16-byte pieces j and j+16 of the 512-byte row: each load is 256
+//       contiguous bytes per token), dot with the G query heads via
+//       v_dot2_f32_f16; a 16-lane DPP sum finishes each score;
+//   softmax: log2 domain; page max over the four rows with row-broadcast
+//       DPP and one v_readlane (no LDS round trips); v_exp_f32;
+//       probabilities rounded to fp16 pairs;
+//   PV: lane owns dims 4*lane..4*lane+3 of all G heads; tokens t and t+4
 //       are paired so one v_dot2_f32_f16 folds two tokens; the pair's
-//       probabilities (fp16x2) come from group r via v_readlane (uniform).
-// All K/V loads are 16- or 8-byte lane loads of 512-byte rows (coalesced).
+//       probabilities come from row t%4 via v_readlane (wave-uniform).
 #include "k_common.h"
 #include "kva_internal.h"
 
@@ -29,224 +34,392 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int G>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
-    const int split = blockIdx.x;
-    const int h = blockIdx.y;
-    const int b = blockIdx.z;
-    const int hkv = a.num_kv_heads;
-    const int nh = a.num_heads;
-    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
-    const int tok_begin = split * a.split_tokens;
-    if (tok_begin >= ctx) return;  // uniform over the workgroup
-    const int tok_end = min(ctx, tok_begin + a.split_tokens);
-    const int32_t *trow =
-        a.table ? a.table + static_cast<size_t>(a.seq_ids[b]) * a.table_stride : nullptr;
+// Sum over the 16 lanes of a DPP row; every lane gets the sum.
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f<kDppQuadXor1>(x);
+    x += dpp_f<kDppQuadXor2>(x);
+    x += dpp_f<kDppRowHalfMirror>(x);
+    x += dpp_f<kDppRowMirror>(x);
+    return x;
+}
 
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int r = lane >> 3;
-    const int j = lane & 7;
-    const size_t row_elems = static_cast<size_t>(hkv) * kHeadDim;
-    const size_t block_elems = kBlockTokens * row_elems;
-    const float qk_scale = kLog2e / 16.0f;  // log2(e) / sqrt(256)
+struct KRegs {
+    uint4 k[4][2];  // tokens r + 4*t4, pieces j and j+16
+};
+struct VRegs {
+    uint2 v[16];    // all 16 tokens, dims 4*lane..4*lane+3
+};
 
-    uint4 qv[G][4];
-    const uint16_t *qb = a.q + (static_cast<size_t>(b) * nh + static_cast<size_t>(h) * G) * kHeadDim;
+// Load a page's K (row stride row_bytes) into registers; rows >= lim read as 0.
+template <bool kFull>
+__device__ __forceinline__ void load_k(KRegs &p, const char *kb, uint32_t koff, int row_bytes,
+                                       int r, int lim) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) qv[g][k] = ld16(qb + g * kHeadDim + 8 * (j + 8 * k));
-
-    float m[G], l[G], acc[G][4];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[g][c] = 0.0f;
-    }
-
-    const int blk_begin = tok_begin >> 4;
-    const int blk_end = (tok_end + 15) >> 4;
-    for (int blk = blk_begin + wave; blk < blk_end; blk += kDecodeWaves) {
-        const size_t page = trow ? static_cast<size_t>(trow[blk]) * block_elems
-                                 : b * a.seq_stride + static_cast<size_t>(blk) * block_elems;
-        const uint16_t *kb = a.k_pool + page + h * kHeadDim;
-        const uint16_t *vb = a.v_pool + page + h * kHeadDim;
-        const int page_tok = blk * kBlockTokens;
-        const int lim = min(kBlockTokens, tok_end - page_tok);  // valid rows of this page
-        uint4 k0[4], k1[4];
-        uint2 vt[16];
-        if (lim == kBlockTokens) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                k0[k] = ld16(kb + r * row_elems + 8 * (j + 8 * k));
-                k1[k] = ld16(kb + (r + 8) * row_elems + 8 * (j + 8 * k));
-            }
-#pragma unroll
-            for (int t = 0; t < 16; ++t) vt[t] = ld8(vb + t * row_elems + 4 * lane);
+    for (int t4 = 0; t4 < 4; ++t4) {
+        const char *base = kb + t4 * 4 * row_bytes + koff;
+        if (kFull || r + 4 * t4 < lim) {
+            p.k[t4][0] = *reinterpret_cast<const uint4 *>(base);
+            p.k[t4][1] = *reinterpret_cast<const uint4 *>(base + 256);
         } else {
-            // Last page of the sequence: rows at or past the length are not
-            // read (a contiguous cache may end there) and count as zeros.
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                k0[k] = (r < lim) ? ld16(kb + r * row_elems + 8 * (j + 8 * k)) : make_uint4(0, 0, 0, 0);
-                k1[k] = (r + 8 < lim) ? ld16(kb + (r + 8) * row_elems + 8 * (j + 8 * k))
-                                      : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int t = 0; t < 16; ++t)
-                vt[t] = (t < lim) ? ld8(vb + t * row_elems + 4 * lane) : make_uint2(0, 0);
-        }
-
-        float s0[G], s1[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float x0 = 0.0f, x1 = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                x0 = dot2(qv[g][k].x, k0[k].x, x0);
-                x0 = dot2(qv[g][k].y, k0[k].y, x0);
-                x0 = dot2(qv[g][k].z, k0[k].z, x0);
-                x0 = dot2(qv[g][k].w, k0[k].w, x0);
-                x1 = dot2(qv[g][k].x, k1[k].x, x1);
-                x1 = dot2(qv[g][k].y, k1[k].y, x1);
-                x1 = dot2(qv[g][k].z, k1[k].z, x1);
-                x1 = dot2(qv[g][k].w, k1[k].w, x1);
-            }
-            s0[g] = group8_sum(x0) * qk_scale;
-            s1[g] = group8_sum(x1) * qk_scale;
-        }
-        if (lim < kBlockTokens) {
-            // Rows past the length get probability exactly 0 (their V is 0).
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                s0[g] = (r < lim) ? s0[g] : -INFINITY;
-                s1[g] = (r + 8 < lim) ? s1[g] : -INFINITY;
-            }
-        }
-
-        uint32_t pp[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float bm = wave_groups_max(fmaxf(s0[g], s1[g]));
-            const float mn = fmaxf(m[g], bm);
-            const float corr = __builtin_amdgcn_exp2f(m[g] - mn);
-            const uint32_t p2 = pack_h2(__builtin_amdgcn_exp2f(s0[g] - mn),
-                                        __builtin_amdgcn_exp2f(s1[g] - mn));
-            pp[g] = p2;
-            l[g] = l[g] * corr + (lo_f(p2) + hi_f(p2));
-            m[g] = mn;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[g][c] *= corr;
-        }
-#pragma unroll
-        for (int rr = 0; rr < 8; ++rr) {
-            const uint2 va = vt[rr];
-            const uint2 vb2 = vt[rr + 8];
-            const uint32_t v0 = (va.x & 0xffffu) | (vb2.x << 16);
-            const uint32_t v1 = (va.x >> 16) | (vb2.x & 0xffff0000u);
-            const uint32_t v2 = (va.y & 0xffffu) | (vb2.y << 16);
-            const uint32_t v3 = (va.y >> 16) | (vb2.y & 0xffff0000u);
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const uint32_t pr = static_cast<uint32_t>(
-                    __builtin_amdgcn_readlane(static_cast<int>(pp[g]), rr * 8));
-                acc[g][0] = dot2(pr, v0, acc[g][0]);
-                acc[g][1] = dot2(pr, v1, acc[g][1]);
-                acc[g][2] = dot2(pr, v2, acc[g][2]);
-                acc[g][3] = dot2(pr, v3, acc[g][3]);
-            }
+            p.k[t4][0] = make_uint4(0, 0, 0, 0);
+            p.k[t4][1] = make_uint4(0, 0, 0, 0);
         }
     }
+}
 
-    // Merge the four waves (LDS), then write the split's partial state or,
-    // with a single split, the normalised output.
-    __shared__ float sm_ml[kDecodeWaves][G][2];
-    __shared__ float4 sm_acc[kDecodeWaves][G][64];
-    __shared__ int sm_last;
+template <bool kFull>
+__device__ __forceinline__ void load_v(VRegs &p, const char *vb, uint32_t voff, int row_bytes,
+                                       int lim) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float lt = wave_groups_sum(l[g]);
-        if (lane == 0) {
-            sm_ml[wave][g][0] = m[g];
-            sm_ml[wave][g][1] = lt;
-        }
-        sm_acc[wave][g][lane] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-    }
-    __syncthreads();
-    const int d = threadIdx.x;  // one output dim per thread
-    const size_t unit0 = (static_cast<size_t>(b) * a.n_splits * hkv + h) * G;  // split 0, head 0
-    const size_t split_stride = static_cast<size_t>(hkv) * G;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float mw[kDecodeWaves];
-        float big = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
-            mw[w] = sm_ml[w][g][0];
-            big = fmaxf(big, mw[w]);
-        }
-        float lt = 0.0f, at = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
-            const float cw = (mw[w] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - big);
-            lt += cw * sm_ml[w][g][1];
-            at += cw * reinterpret_cast<const float *>(&sm_acc[w][g][0])[d];
-        }
-        if (a.n_splits == 1) {
-            a.out[(static_cast<size_t>(b) * nh + h * G + g) * kHeadDim + d] = f2h(at / lt);
-        } else {
-            const size_t unit = unit0 + split * split_stride + g;
-            a.ws_acc[unit * kHeadDim + d] = at;
-            if (d == 0) {
-                a.ws_ml[unit * 2] = big;
-                a.ws_ml[unit * 2 + 1] = lt;
-            }
-        }
-    }
-    if (a.n_splits == 1) return;
-
-    // Split-K combine, fused: the last workgroup of this (sequence, KV head)
-    // to finish merges every split.  Partials are released at agent scope
-    // before the arrival count and acquired after it (the L2s of different
-    // XCDs are not coherent without these fences); the last arrival resets
-    // the counter for the next launch.
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int *ctr = a.counters + static_cast<size_t>(b) * hkv + h;
-        const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = prev == ns - 1;
-        if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sm_last = last;
-    }
-    __syncthreads();
-    if (!sm_last) return;
-    __threadfence();
-    const int ns = (ctx + a.split_tokens - 1) / a.split_tokens;
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float big = -INFINITY;
-        for (int sp = 0; sp < ns; ++sp)
-            big = fmaxf(big, a.ws_ml[(unit0 + sp * split_stride + g) * 2]);
-        float lt = 0.0f, at = 0.0f;
-        for (int sp = 0; sp < ns; ++sp) {
-            const size_t u = unit0 + sp * split_stride + g;
-            const float c = __builtin_amdgcn_exp2f(a.ws_ml[u * 2] - big);
-            lt += c * a.ws_ml[u * 2 + 1];
-            at += c * a.ws_acc[u * kHeadDim + d];
-        }
-        a.out[(static_cast<size_t>(b) * nh + h * G + g) * kHeadDim + d] = f2h(at / lt);
+    for (int t = 0; t < 16; ++t) {
+        if (kFull || t < lim)
+            p.v[t] = *reinterpret_cast<const uint2 *>(vb + t * row_bytes + voff);
+        else
+            p.v[t] = make_uint2(0, 0);
     }
 }
 
 template <int G>
+struct WaveState {
+    float m[G], l[G], acc[G][4];
+};
+
+// Fold one page into the wave's online-softmax state.  lim < 16 masks rows.
+template <int G, bool kFull>
+__device__ __forceinline__ void compute_page(WaveState<G> &st, const KRegs &p, const VRegs &pv,
+                                             const uint4 (&qv)[G][2], int r, int lim) {
+    const float qk_scale = kLog2e / 16.0f;  // log2(e) / sqrt(256)
+    float s[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int t4 = 0; t4 < 4; ++t4) {
+            float x = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                x = dot2(qv[g][q].x, p.k[t4][q].x, x);
+                x = dot2(qv[g][q].y, p.k[t4][q].y, x);
+                x = dot2(qv[g][q].z, p.k[t4][q].z, x);
+                x = dot2(qv[g][q].w, p.k[t4][q].w, x);
+            }
+            s[g][t4] = row16_sum(x) * qk_scale;
+        }
+    if (!kFull) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) s[g][t4] = (r + 4 * t4 < lim) ? s[g][t4] : -INFINITY;
+    }
+    // Page max per head: the 16 lanes of a row agree, so a row-broadcast DPP
+    // max (rows 1,3 <- rows 0,2; then rows 2,3 <- row 1) leaves the wave max
+    // in lane 63; all heads are reduced together to overlap the DPP hazards.
+    float bm[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) bm[g] = fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3]));
+#pragma unroll
+    for (int g = 0; g < G; ++g) bm[g] = fmaxf(bm[g], dpp_masked_f<kDppRowBcast15, 0xA>(bm[g]));
+#pragma unroll
+    for (int g = 0; g < G; ++g) bm[g] = fmaxf(bm[g], dpp_masked_f<kDppRowBcast31, 0xC>(bm[g]));
+    uint32_t pa[G], pb[G];  // fp16 pairs: tokens (r, r+4) and (r+8, r+12)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float mn = fmaxf(st.m[g], __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                __builtin_bit_cast(int, bm[g]), 63)));
+        const float corr = __builtin_amdgcn_exp2f(st.m[g] - mn);
+        pa[g] = pack_h2(__builtin_amdgcn_exp2f(s[g][0] - mn), __builtin_amdgcn_exp2f(s[g][1] - mn));
+        pb[g] = pack_h2(__builtin_amdgcn_exp2f(s[g][2] - mn), __builtin_amdgcn_exp2f(s[g][3] - mn));
+        st.l[g] = st.l[g] * corr + ((lo_f(pa[g]) + hi_f(pa[g])) + (lo_f(pb[g]) + hi_f(pb[g])));
+        st.m[g] = mn;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) st.acc[g][c] *= corr;
+    }
+#pragma unroll
+    for (int pr = 0; pr < 8; ++pr) {
+        // Pair pr: row rr = pr & 3, tokens (rr, rr+4) or (rr+8, rr+12).
+        const int rr = pr & 3;
+        const int t0 = rr + (pr >> 2) * 8;
+        const uint2 va = pv.v[t0];
+        const uint2 vb = pv.v[t0 + 4];
+        const uint32_t v0 = (va.x & 0xffffu) | (vb.x << 16);
+        const uint32_t v1 = (va.x >> 16) | (vb.x & 0xffff0000u);
+        const uint32_t v2 = (va.y & 0xffffu) | (vb.y << 16);
+        const uint32_t v3 = (va.y >> 16) | (vb.y & 0xffff0000u);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const uint32_t src = (pr >> 2) ? pb[g] : pa[g];
+            const uint32_t pp =
+                static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(src), rr * 16));
+            st.acc[g][0] = dot2(pp, v0, st.acc[g][0]);
+            st.acc[g][1] = dot2(pp, v1, st.acc[g][1]);
+            st.acc[g][2] = dot2(pp, v2, st.acc[g][2]);
+            st.acc[g][3] = dot2(pp, v3, st.acc[g][3]);
+        }
+    }
+}
+
+// First page of workgroup w when P pages are shared by W workgroups.
+__device__ __forceinline__ int wg_start(int w, int P, int W) {
+    return static_cast<int>(static_cast<int64_t>(w) * P / W);
+}
+
+// The workgroup whose page range holds page p.
+__device__ __forceinline__ int wg_of_page(int p, int P, int W) {
+    int w = static_cast<int>(static_cast<int64_t>(p) * W / P);
+    while (w + 1 < W && wg_start(w + 1, P, W) <= p) ++w;
+    return w;
+}
+
+// Pages of all (sequence, kv head) units before sequence b (units are
+// ordered sequence-major, then kv head).
+__device__ __forceinline__ int seq_page_base(const DecodeArgs &a, int b, int npg) {
+    return a.pre_seq ? a.pre_seq[b] : b * a.num_kv_heads * npg;
+}
+
+// Stream-K decode: the pages of every (sequence, kv head) unit are laid end
+// to end and workgroup w takes pages [wg_start(w), wg_start(w+1)) — equal
+// shares, whatever the ragged lengths.  A workgroup walks the unit segments
+// of its range; a unit it covers whole is written out directly, a unit cut
+// by a range boundary leaves a partial (m, l, acc) in slot 2w (the range's
+// first unit) or 2w+1 (its last unit) for combine_kernel.
+template <int G>
+__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+    const int w = blockIdx.x;
+    const int W = a.n_wg;
+    const int P = a.total_pages;
+    const int p_begin = wg_start(w, P, W);
+    const int p_end = wg_start(w + 1, P, W);
+    if (p_begin >= p_end) return;  // uniform over the workgroup
+    const int hkv = a.num_kv_heads;
+    const int nh = a.num_heads;
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane >> 4;
+    const int j = lane & 15;
+    const int row_bytes = hkv * kHeadDim * 2;
+    const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
+    const uint32_t koff = r * row_bytes + 16 * j;
+    const uint32_t voff = 8 * lane;
+
+    // Sequence holding p_begin: the last b with base(b) <= p_begin.
+    int b;
+    if (a.pre_seq) {
+        int lo = 0, hi = a.n_seqs - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (a.pre_seq[mid] <= p_begin) lo = mid; else hi = mid - 1;
+        }
+        b = lo;
+    } else {
+        b = p_begin / (hkv * ((a.ctx_len_const + 15) >> 4));
+    }
+
+    __shared__ float sm_ml[kDecodeWaves][G][2];
+    __shared__ float4 sm_acc[kDecodeWaves][G][64];
+    int p = p_begin;
+    bool first_seg = true;
+    while (p < p_end) {
+        const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
+        const int npg = (ctx + 15) >> 4;
+        const int base_b = seq_page_base(a, b, npg);
+        if (npg == 0 || p >= base_b + hkv * npg) {  // empty or finished sequence
+            ++b;
+            continue;
+        }
+        const int h = (p - base_b) / npg;
+        const int pg0 = p - base_b - h * npg;
+        const int seg_end = min(base_b + (h + 1) * npg, p_end);
+        const int pg1 = pg0 + (seg_end - p);
+
+        const int32_t *trow =
+            a.table ? a.table + static_cast<size_t>(a.seq_ids[b]) * a.table_stride : nullptr;
+        const size_t seq_base = a.table ? 0 : static_cast<size_t>(b) * a.seq_stride * 2;
+        const char *kpool = reinterpret_cast<const char *>(a.k_pool) + seq_base + h * kHeadDim * 2;
+        const char *vpool = reinterpret_cast<const char *>(a.v_pool) + seq_base + h * kHeadDim * 2;
+
+        uint4 qv[G][2];
+        const uint16_t *qb =
+            a.q + (static_cast<size_t>(b) * nh + static_cast<size_t>(h) * G) * kHeadDim;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            qv[g][0] = ld16(qb + g * kHeadDim + 8 * j);
+            qv[g][1] = ld16(qb + g * kHeadDim + 8 * (j + 16));
+        }
+        WaveState<G> st;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            st.m[g] = -INFINITY;
+            st.l[g] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) st.acc[g][c] = 0.0f;
+        }
+
+        // This wave's pages of the segment: first, first+4, ...  All are full
+        // except the unit's last page when the length is not a page multiple.
+        const int first = pg0 + wave;
+        const int n_pages = first < pg1 ? (pg1 - first + kDecodeWaves - 1) / kDecodeWaves : 0;
+        const int last_lim = ctx - (npg - 1) * kBlockTokens;
+        const bool owns_partial = last_lim < kBlockTokens && n_pages > 0 &&
+                                  first + (n_pages - 1) * kDecodeWaves == npg - 1;
+        const int n_full = n_pages - (owns_partial ? 1 : 0);
+        auto page_off = [&](int blk) -> size_t {
+            const int pb = trow ? __builtin_amdgcn_readfirstlane(trow[blk]) : blk;
+            return static_cast<size_t>(pb) * page_bytes;
+        };
+
+        // K of the next page is prefetched into the idle one of two register
+        // buffers; V of the current page is issued first and lands during QK.
+        KRegs KA, KB;
+        VRegs V;
+#if KVA_DEEP_PREFETCH
+        VRegs V2;
+        if (n_full > 0) {
+            load_k<true>(KA, kpool + page_off(first), koff, row_bytes, r, kBlockTokens);
+            load_v<true>(V, vpool + page_off(first), voff, row_bytes, kBlockTokens);
+        }
+        for (int i = 0; i < n_full; i += 2) {
+            if (i + 1 < n_full) {
+                const size_t o = page_off(first + (i + 1) * kDecodeWaves);
+                load_k<true>(KB, kpool + o, koff, row_bytes, r, kBlockTokens);
+                load_v<true>(V2, vpool + o, voff, row_bytes, kBlockTokens);
+            }
+            compute_page<G, true>(st, KA, V, qv, r, kBlockTokens);
+            if (i + 1 >= n_full) break;
+            if (i + 2 < n_full) {
+                const size_t o = page_off(first + (i + 2) * kDecodeWaves);
+                load_k<true>(KA, kpool + o, koff, row_bytes, r, kBlockTokens);
+                load_v<true>(V, vpool + o, voff, row_bytes, kBlockTokens);
+            }
+            compute_page<G, true>(st, KB, V2, qv, r, kBlockTokens);
+        }
+#else
+        if (n_full > 0) load_k<true>(KA, kpool + page_off(first), koff, row_bytes, r, kBlockTokens);
+        for (int i = 0; i < n_full; i += 2) {
+            load_v<true>(V, vpool + page_off(first + i * kDecodeWaves), voff, row_bytes, kBlockTokens);
+            if (i + 1 < n_full)
+                load_k<true>(KB, kpool + page_off(first + (i + 1) * kDecodeWaves), koff, row_bytes, r,
+                             kBlockTokens);
+            compute_page<G, true>(st, KA, V, qv, r, kBlockTokens);
+            if (i + 1 >= n_full) break;
+            load_v<true>(V, vpool + page_off(first + (i + 1) * kDecodeWaves), voff, row_bytes,
+                         kBlockTokens);
+            if (i + 2 < n_full)
+                load_k<true>(KA, kpool + page_off(first + (i + 2) * kDecodeWaves), koff, row_bytes, r,
+                             kBlockTokens);
+            compute_page<G, true>(st, KB, V, qv, r, kBlockTokens);
+        }
+#endif
+        if (owns_partial) {
+            const size_t o = page_off(npg - 1);
+            load_k<false>(KA, kpool + o, koff, row_bytes, r, last_lim);
+            load_v<false>(V, vpool + o, voff, row_bytes, last_lim);
+            compute_page<G, false>(st, KA, V, qv, r, last_lim);
+        }
+
+        // Merge the four waves through LDS; write the output (whole unit) or
+        // this range's partial for the unit.
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float lt = st.l[g];  // rows hold disjoint tokens: sum the four rows
+            lt += __shfl_xor(lt, 16);
+            lt += __shfl_xor(lt, 32);
+            if (lane == 0) {
+                sm_ml[wave][g][0] = st.m[g];
+                sm_ml[wave][g][1] = lt;
+            }
+            sm_acc[wave][g][lane] = make_float4(st.acc[g][0], st.acc[g][1], st.acc[g][2], st.acc[g][3]);
+        }
+        __syncthreads();
+        const bool whole = pg0 == 0 && pg1 == npg;
+        const int slot = 2 * w + (first_seg ? 0 : 1);
+        const int d = threadIdx.x;  // one output dim per thread
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float mw[kDecodeWaves];
+            float big = -INFINITY;
+#pragma unroll
+            for (int wv = 0; wv < kDecodeWaves; ++wv) {
+                mw[wv] = sm_ml[wv][g][0];
+                big = fmaxf(big, mw[wv]);
+            }
+            float lt = 0.0f, at = 0.0f;
+#pragma unroll
+            for (int wv = 0; wv < kDecodeWaves; ++wv) {
+                const float cw = (mw[wv] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[wv] - big);
+                lt += cw * sm_ml[wv][g][1];
+                at += cw * reinterpret_cast<const float *>(&sm_acc[wv][g][0])[d];
+            }
+            if (whole) {
+                a.out[(static_cast<size_t>(b) * nh + h * G + g) * kHeadDim + d] = f2h(at / lt);
+            } else {
+                const size_t u = static_cast<size_t>(slot) * G + g;
+                a.ws_acc[u * kHeadDim + d] = at;
+                if (d == 0) {
+                    a.ws_ml[u * 2] = big;
+                    a.ws_ml[u * 2 + 1] = lt;
+                }
+            }
+        }
+        __syncthreads();  // LDS is reused by the next segment
+        p = seg_end;
+        first_seg = false;
+    }
+}
+
+// Merge the partials of one (unit, query head of its group) whose pages were
+// cut across workgroups: 64 lanes x 4 dims.  A separate launch (stream order
+// makes the partials visible), so no cross-workgroup fences are needed: an
+// agent-scope release on every decode workgroup costs an L2 writeback per
+// workgroup on multi-XCD parts.
+template <int G>
+__global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
+    const int u = blockIdx.x;
+    const int g = blockIdx.y;
+    const int hkv = a.num_kv_heads;
+    const int b = u / hkv;
+    const int h = u - b * hkv;
+    const int lane = threadIdx.x;
+    const int W = a.n_wg;
+    const int P = a.total_pages;
+    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
+    const int npg = (ctx + 15) >> 4;
+    if (npg == 0) return;
+    const int first = seq_page_base(a, b, npg) + h * npg;
+    const int w0 = wg_of_page(first, P, W);
+    const int w1 = wg_of_page(first + npg - 1, P, W);
+    if (w0 == w1) return;  // one workgroup covered the unit and wrote it
+    float big = -INFINITY;
+    for (int w = w0; w <= w1; ++w) {
+        const int slot = 2 * w + (first <= wg_start(w, P, W) ? 0 : 1);
+        big = fmaxf(big, a.ws_ml[(static_cast<size_t>(slot) * G + g) * 2]);
+    }
+    float lt = 0.0f;
+    float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int w = w0; w <= w1; ++w) {
+        const int slot = 2 * w + (first <= wg_start(w, P, W) ? 0 : 1);
+        const size_t s = static_cast<size_t>(slot) * G + g;
+        const float c = __builtin_amdgcn_exp2f(a.ws_ml[s * 2] - big);
+        lt += c * a.ws_ml[s * 2 + 1];
+        const float4 v = reinterpret_cast<const float4 *>(a.ws_acc + s * kHeadDim)[lane];
+        at.x += c * v.x;
+        at.y += c * v.y;
+        at.z += c * v.z;
+        at.w += c * v.w;
+    }
+    const float inv = 1.0f / lt;
+    uint2 o;
+    o.x = pack_h2(at.x * inv, at.y * inv);
+    o.y = pack_h2(at.z * inv, at.w * inv);
+    *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(b) * a.num_heads + h * G + g) * kHeadDim +
+                               4 * lane) = o;
+}
+
+template <int G>
 hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
-    const dim3 grid(a.n_splits, a.num_kv_heads, a.n_seqs);
-    hipLaunchKernelGGL(decode_kernel<G>, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL(decode_kernel<G>, dim3(a.n_wg), dim3(256), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !a.ws_acc) return e;
+    hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -49,7 +49,9 @@ int hip_fail(hipError_t e, const char *what) {
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 constexpr int kStageSlots = 4;
-constexpr int kTargetDecodeUnits = 2048;  // workgroups a decode launch aims for
+constexpr int kDecodeWgPerCu = 1;   // stream-K decode workgroups per CU
+constexpr int kMinPagesPerWg = 8;   // two pages per wave at least
+constexpr int kMaxGroup = 8;        // largest GQA group the kernels take
 
 }  // namespace
 
@@ -70,8 +72,8 @@ struct kva_cache {
     size_t aux_bytes = 0;
     float *d_ws_acc = nullptr;
     float *d_ws_ml = nullptr;
-    int32_t *d_counters = nullptr;  // [max_seqs][num_kv_heads] split arrivals
-    int32_t ws_max_splits = 0;
+    int32_t max_wg = 0;  // decode workgroups the partial workspace can serve
+    int32_t n_cu = 0;
 
     // pinned staging ring
     uint8_t *h_stage[kStageSlots] = {};
@@ -92,13 +94,13 @@ struct kva_cache {
     // current step plan
     bool step_valid = false;
     int32_t st_n_seqs = 0, st_n_tok = 0, st_max_ctx = 0, st_max_new = 0, st_max_pos = 0;
-    int64_t st_sum_ctx = 0;
+    int32_t st_total_pages = 0;  // pages of all (sequence, kv head) units
     bool st_all_one = false, st_has_bits = false;
     size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
-           off_tslot = 0, off_tpos = 0, off_bits = 0;
+           off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0;
 
-    int32_t split_user = 0;
-    int32_t last_split = 0, last_nsplits = 0;
+    int32_t split_user = 0;  // decode tokens per workgroup (0 = automatic)
+    int32_t last_split = 0, last_nwg = 0;
 };
 
 namespace {
@@ -233,25 +235,19 @@ T *at(uint8_t *base, size_t off) {
     return reinterpret_cast<T *>(base + off);
 }
 
-// Choose tokens per split and the split count for a decode launch.
-void choose_split(const kva_cache *c, int32_t max_ctx, int64_t sum_ctx, int32_t *split,
-                  int32_t *n_splits) {
-    const int64_t q = kva::kSplitQuantum;
-    int64_t s;
-    if (c->split_user > 0) {
-        s = c->split_user;
-    } else {
-        s = (sum_ctx * c->cfg.num_kv_heads + kTargetDecodeUnits - 1) / kTargetDecodeUnits;
-        s = std::max<int64_t>(q, std::min<int64_t>(4096, (s + q - 1) / q * q));
-    }
-    int64_t ns = (max_ctx + s - 1) / s;
-    if (ns > c->ws_max_splits) {
-        s = (max_ctx + c->ws_max_splits - 1) / c->ws_max_splits;
-        s = (s + q - 1) / q * q;
-        ns = (max_ctx + s - 1) / s;
-    }
-    *split = static_cast<int32_t>(s);
-    *n_splits = static_cast<int32_t>(std::max<int64_t>(1, ns));
+// Workgroups for a stream-K decode over `pages` pages: one per CU by default
+// (each then streams long runs of pages), or pages*16/split_user when a
+// token count per workgroup was set; never more than the workspace holds or
+// than there are pages, and at least kMinPagesPerWg pages each.
+int32_t choose_wg(const kva_cache *c, int64_t pages) {
+    int64_t w;
+    if (c->split_user > 0)
+        w = (pages * kva::kBlockTokens + c->split_user - 1) / c->split_user;
+    else
+        w = static_cast<int64_t>(c->n_cu) * kDecodeWgPerCu;
+    w = std::min<int64_t>(w, (pages + kMinPagesPerWg - 1) / kMinPagesPerWg);
+    w = std::min<int64_t>(w, c->max_wg);
+    return static_cast<int32_t>(std::max<int64_t>(1, w));
 }
 
 }  // namespace
@@ -280,10 +276,8 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
     c->used.assign(cfg->max_blocks, 0);
     c->free_list.resize(cfg->max_blocks);
     for (int32_t i = 0; i < cfg->max_blocks; ++i) c->free_list[i] = cfg->max_blocks - 1 - i;
-    // Split-K workspace: splits of at least 256 tokens always fit.
-    c->ws_max_splits = static_cast<int32_t>(std::max<size_t>(16, (mbps * kva::kBlockTokens + 255) / 256));
-    // Step plan: 4 per-sequence arrays + offsets + 3 per-token arrays + bits.
-    c->step_bytes = round_up(sizeof(int32_t) * (4 * static_cast<size_t>(cfg->max_seqs) + 1), 256) +
+    // Step plan: 5 per-sequence arrays + 3 per-token arrays + bits.
+    c->step_bytes = round_up(sizeof(int32_t) * (5 * static_cast<size_t>(cfg->max_seqs) + 2), 256) +
                     round_up(sizeof(int32_t) * 3 * static_cast<size_t>(cfg->max_step_tokens), 256) +
                     round_up(sizeof(uint64_t) * static_cast<size_t>(cfg->max_step_tokens), 256) + 1024;
     const size_t patch_cap = std::max<size_t>(4096, cfg->max_seqs + cfg->max_step_tokens);
@@ -309,16 +303,19 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
         if ((e = hipMemset(c->d_table, 0, tbytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMemset(table)"));
         if ((e = hipMalloc(&c->d_step, c->step_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(step)"));
         if ((e = hipMalloc(&c->d_aux, c->aux_bytes)) != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(aux)"));
-        const size_t units = static_cast<size_t>(cfg->max_seqs) * c->ws_max_splits * cfg->num_heads;
+        int dev = 0, ncu = 0;
+        if ((e = hipGetDevice(&dev)) != hipSuccess) return cleanup(hip_fail(e, "hipGetDevice"));
+        if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess)
+            return cleanup(hip_fail(e, "hipDeviceGetAttribute(CU count)"));
+        c->n_cu = std::max(1, ncu);
+        // Partial slots: two per decode workgroup, each [group][256] floats;
+        // up to four workgroups per CU can be requested.
+        c->max_wg = 4 * c->n_cu;
+        const size_t units = static_cast<size_t>(2) * c->max_wg * kMaxGroup;
         if ((e = hipMalloc(&c->d_ws_acc, units * kva::kHeadDim * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(workspace)"));
         if ((e = hipMalloc(&c->d_ws_ml, units * 2 * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(workspace ml)"));
-        const size_t cbytes = static_cast<size_t>(cfg->max_seqs) * cfg->num_kv_heads * sizeof(int32_t);
-        if ((e = hipMalloc(&c->d_counters, cbytes)) != hipSuccess)
-            return cleanup(hip_fail(e, "hipMalloc(split counters)"));
-        if ((e = hipMemset(c->d_counters, 0, cbytes)) != hipSuccess)
-            return cleanup(hip_fail(e, "hipMemset(split counters)"));
         for (int i = 0; i < kStageSlots; ++i) {
             if ((e = hipHostMalloc(reinterpret_cast<void **>(&c->h_stage[i]), c->stage_bytes,
                                    hipHostMallocDefault)) != hipSuccess)
@@ -347,7 +344,6 @@ int kva_destroy(kva_cache *c) {
         (void)hipFree(c->d_aux);
         (void)hipFree(c->d_ws_acc);
         (void)hipFree(c->d_ws_ml);
-        (void)hipFree(c->d_counters);
     }
     delete c;
     return KVA_OK;
@@ -554,7 +550,8 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     const size_t o_ctx = o_seq + sizeof(int32_t) * n_seqs;
     const size_t o_start = o_ctx + sizeof(int32_t) * n_seqs;
     const size_t o_tokoff = o_start + sizeof(int32_t) * n_seqs;
-    const size_t o_tseq = round_up(o_tokoff + sizeof(int32_t) * (n_seqs + 1), 16);
+    const size_t o_pre = o_tokoff + sizeof(int32_t) * (n_seqs + 1);
+    const size_t o_tseq = round_up(o_pre + sizeof(int32_t) * (n_seqs + 1), 16);
     const size_t o_tslot = round_up(o_tseq + sizeof(int32_t) * n_tok, 16);
     const size_t o_tpos = round_up(o_tslot + sizeof(int32_t) * n_tok, 16);
     const size_t o_bits = round_up(o_tpos + sizeof(int32_t) * n_tok, 16);
@@ -573,9 +570,9 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     int32_t *p_seq = at<int32_t>(h, o_seq), *p_ctx = at<int32_t>(h, o_ctx),
             *p_start = at<int32_t>(h, o_start), *p_off = at<int32_t>(h, o_tokoff),
             *p_tseq = at<int32_t>(h, o_tseq), *p_tslot = at<int32_t>(h, o_tslot),
-            *p_tpos = at<int32_t>(h, o_tpos);
+            *p_tpos = at<int32_t>(h, o_tpos), *p_pre = at<int32_t>(h, o_pre);
     int32_t max_ctx = 0, max_new = 0, max_pos = 0;
-    int64_t sum_ctx = 0;
+    int64_t pages = 0;
     bool all_one = true;
     int32_t t = 0;
     for (int32_t b = 0; b < n_seqs; ++b) {
@@ -594,10 +591,12 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
         c->len[s] = start + n_new[b];
         max_ctx = std::max(max_ctx, p_ctx[b]);
         max_new = std::max(max_new, n_new[b]);
-        sum_ctx += p_ctx[b];
+        p_pre[b] = static_cast<int32_t>(pages);
+        pages += static_cast<int64_t>(c->cfg.num_kv_heads) * ((p_ctx[b] + kva::kBlockTokens - 1) / kva::kBlockTokens);
         all_one = all_one && n_new[b] == 1;
     }
     p_off[n_seqs] = t;
+    p_pre[n_seqs] = static_cast<int32_t>(pages);
     if (tree_bits) std::memcpy(h + o_bits, tree_bits, sizeof(uint64_t) * n_tok);
 
     if (!c->host_only) {
@@ -617,12 +616,13 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->off_tslot = o_tslot;
     c->off_tpos = o_tpos;
     c->off_bits = o_bits;
+    c->off_pre = o_pre;
     c->st_n_seqs = n_seqs;
     c->st_n_tok = static_cast<int32_t>(n_tok);
     c->st_max_ctx = max_ctx;
     c->st_max_new = max_new;
     c->st_max_pos = max_pos;
-    c->st_sum_ctx = sum_ctx;
+    c->st_total_pages = static_cast<int32_t>(pages);
     c->st_all_one = all_one;
     c->st_has_bits = tree_bits != nullptr;
     c->step_valid = true;
@@ -683,8 +683,19 @@ int kva_set_decode_split(kva_cache *c, int32_t split_tokens) {
 int kva_get_decode_split(const kva_cache *c, int32_t *split_tokens, int32_t *n_splits) {
     if (!c || !split_tokens || !n_splits) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
     *split_tokens = c->last_split;
-    *n_splits = c->last_nsplits;
+    *n_splits = c->last_nwg;
     return KVA_OK;
+}
+
+// Fill the stream-K fields of a decode launch over `pages` pages.
+static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_t group) {
+    a.total_pages = static_cast<int32_t>(pages);
+    a.n_wg = choose_wg(c, pages);
+    a.ws_acc = c->d_ws_acc;
+    a.ws_ml = c->d_ws_ml;
+    (void)group;
+    c->last_nwg = a.n_wg;
+    c->last_split = static_cast<int32_t>((pages * kva::kBlockTokens + a.n_wg - 1) / a.n_wg);
 }
 
 int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
@@ -703,15 +714,11 @@ int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream
     a.table_stride = c->cfg.max_blocks_per_seq;
     a.seq_ids = at<int32_t>(c->d_step, c->off_seq);
     a.ctx_lens = at<int32_t>(c->d_step, c->off_ctx);
+    a.pre_seq = at<int32_t>(c->d_step, c->off_pre);
     a.n_seqs = c->st_n_seqs;
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
-    choose_split(c, c->st_max_ctx, c->st_sum_ctx, &a.split_tokens, &a.n_splits);
-    c->last_split = a.split_tokens;
-    c->last_nsplits = a.n_splits;
-    a.ws_acc = c->d_ws_acc;
-    a.ws_ml = c->d_ws_ml;
-    a.counters = c->d_counters;
+    set_stream_k(c, a, c->st_total_pages, c->group);
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;
@@ -891,23 +898,15 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *k_base, const
     a.n_seqs = batch;
     a.num_heads = num_heads;
     a.num_kv_heads = num_kv_heads;
-    a.split_tokens = (kv_seq_len + kva::kSplitQuantum - 1) / kva::kSplitQuantum * kva::kSplitQuantum;
-    a.n_splits = 1;
+    // Every sequence has the same length: the page prefix sums are implicit.
+    const int64_t unit_pages = (kv_seq_len + kva::kBlockTokens - 1) / kva::kBlockTokens;
+    const int64_t pages = unit_pages * num_kv_heads * batch;
     if (ws) {
-        int32_t split, ns;
-        choose_split(ws, kv_seq_len, static_cast<int64_t>(kv_seq_len) * batch, &split, &ns);
-        // The workspace holds max_seqs * ws_max_splits * cfg.num_heads partial rows.
-        if (ns > 1 &&
-            static_cast<int64_t>(ns) * num_heads * batch <=
-                static_cast<int64_t>(ws->ws_max_splits) * ws->cfg.num_heads * ws->cfg.max_seqs &&
-            static_cast<int64_t>(batch) * num_kv_heads <=
-                static_cast<int64_t>(ws->cfg.max_seqs) * ws->cfg.num_kv_heads) {
-            a.split_tokens = split;
-            a.n_splits = ns;
-            a.ws_acc = ws->d_ws_acc;
-            a.ws_ml = ws->d_ws_ml;
-            a.counters = ws->d_counters;
-        }
+        set_stream_k(ws, a, pages, g);
+    } else {
+        // No workspace: one workgroup per (sequence, kv head), written whole.
+        a.total_pages = static_cast<int32_t>(pages);
+        a.n_wg = batch * num_kv_heads;
     }
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));

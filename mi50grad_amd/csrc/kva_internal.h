@@ -63,15 +63,17 @@ struct DecodeArgs {
     size_t seq_stride;        // contiguous cache: elements between sequences
     const int32_t *seq_ids;   // device [n_seqs] (ignored when table == null)
     const int32_t *ctx_lens;  // device [n_seqs] (null: use ctx_len_const)
+    const int32_t *pre_seq;   // device [n_seqs+1]: pages of all units of earlier
+                              // sequences (null: every sequence has ctx_len_const)
     int32_t ctx_len_const;
     int32_t n_seqs;
     int32_t num_heads;
     int32_t num_kv_heads;
-    int32_t split_tokens;     // multiple of kSplitQuantum
-    int32_t n_splits;         // grid.x; 1 = outputs written directly
-    float *ws_acc;            // [n_seqs][n_splits][Hkv][G][256] (split mode)
-    float *ws_ml;             // [n_seqs][n_splits][Hkv][G][2]
-    int32_t *counters;        // [n_seqs][Hkv] split arrivals, zero between launches
+    int32_t total_pages;      // pages of all (sequence, kv head) units
+    int32_t n_wg;             // workgroups sharing the pages (stream-K)
+    float *ws_acc;            // [2*n_wg][G][256] partial slots; null = every
+                              // unit is whole in one workgroup (no combine)
+    float *ws_ml;             // [2*n_wg][G][2]
     uint16_t *out;            // [n_seqs][H][256]
 };
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);

@@ -49,11 +49,17 @@ def test_decode_c1_golden(device):
     fx = np.load(Path(__file__).resolve().parent / "golden" / "c1_golden.npz")
     say("decode c1 golden")
     cache, _, _ = build_cache([0], [list(range(16))], extra_rows=256, fill=False)
-    # Cache rows 0..254 from the fixture, written through the row pointers.
-    for s in range(255):
+    # Cache rows 0..254 from the fixture; the host arrays stay referenced
+    # until the copies return.
+    kc = np.ascontiguousarray(fx["k_cache"])
+    vc = np.ascontiguousarray(fx["v_cache"])
+    for s in (0, 100, 254):  # through the row pointers (KVCache.get_kv_ptr's contract)
         kp, vp = cache.row_ptr(0, 0, s)
-        _lib.call("kva_memcpy_h2d", kp, np.ascontiguousarray(fx["k_cache"][s]).ctypes.data, HKV * D * 2)
-        _lib.call("kva_memcpy_h2d", vp, np.ascontiguousarray(fx["v_cache"][s]).ctypes.data, HKV * D * 2)
+        _lib.call("kva_memcpy_h2d", kp, kc[s].ctypes.data, HKV * D * 2)
+        _lib.call("kva_memcpy_h2d", vp, vc[s].ctypes.data, HKV * D * 2)
+    kp0, vp0 = cache.row_ptr(0, 0, 0)  # pages 0..15 are consecutive: rows are contiguous
+    _lib.call("kva_memcpy_h2d", kp0, kc.ctypes.data, kc.nbytes)
+    _lib.call("kva_memcpy_h2d", vp0, vc.ctypes.data, vc.nbytes)
     cache.set_len(0, 255)
     tables = Tables(device, 256)
     dq = device.array(fx["q"])
@@ -83,6 +89,26 @@ def test_decode_ragged_permuted(device, split):
     got, exp, *_ = run_decode_step(device, cache, kr, vr, lengths, rng, tables, split=split)
     err = max_err(got, exp)
     assert err <= TOL, (err, cache.decode_split())
+    cache.destroy()
+
+
+@pytest.mark.parametrize("split", [0, 64, 128, 256])
+def test_decode_many_short_sequences(device, split):
+    """Workgroup page ranges that start, end and span many (sequence, kv head)
+    units: lengths 0..47 plus a long one, permuted pages."""
+    rng = np.random.default_rng(300 + split)
+    lengths = list(range(48)) + [3000]
+    nblk = [(L + 1 + 15) // 16 for L in lengths]
+    perm = rng.permutation(sum(nblk))
+    ids, o = [], 0
+    for n in nblk:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say(f"decode many short split={split}")
+    cache, kr, vr = build_cache(lengths, ids, extra_rows=1, rng=rng)
+    tables = Tables(device, 4096)
+    got, exp, *_ = run_decode_step(device, cache, kr, vr, lengths, rng, tables, split=split)
+    assert max_err(got, exp) <= TOL, cache.decode_split()
     cache.destroy()
 
 
