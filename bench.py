@@ -295,7 +295,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic(f"decode_{args.workload}_traffic.json"),
-                     "kernel": "decode_kernel<6>", "avg_us": r["decode_avg_us"],
+                     "kernel": "kva_decode = decode_kernel<6> + combine_kernel<6> (one stream, "
+                               "HIP events around the call)",
+                     "avg_us": r["decode_avg_us"],
                      "alg_bytes_per_launch": r["alg_bytes_decode_launch"]},
     }
     if not args.no_cpu_baseline:
