@@ -72,6 +72,9 @@ struct kva_cache {
     size_t aux_bytes = 0;
     float *d_ws_acc = nullptr;
     float *d_ws_ml = nullptr;
+    float *d_mq_acc = nullptr;  // multi-query partial slots [2*mq_max_wg][8][16][256]
+    float *d_mq_ml = nullptr;
+    int32_t mq_max_wg = 0;
     int32_t max_wg = 0;  // decode workgroups the partial workspace can serve
     int32_t n_cu = 0;
 
@@ -95,6 +98,9 @@ struct kva_cache {
     bool step_valid = false;
     int32_t st_n_seqs = 0, st_n_tok = 0, st_max_ctx = 0, st_max_new = 0, st_max_pos = 0;
     int32_t st_total_pages = 0;  // pages of all (sequence, kv head) units
+    int32_t st_mq_units = 0;     // (sequence, 16-token tile, kv head) units
+    int32_t st_mq_blocks = 0;    // 32-key blocks of all multi-query units
+    size_t off_upre = 0, off_mqpre = 0;
     bool st_all_one = false, st_has_bits = false;
     size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
            off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0;
@@ -277,7 +283,11 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
     c->free_list.resize(cfg->max_blocks);
     for (int32_t i = 0; i < cfg->max_blocks; ++i) c->free_list[i] = cfg->max_blocks - 1 - i;
     // Step plan: 5 per-sequence arrays + 3 per-token arrays + bits.
-    c->step_bytes = round_up(sizeof(int32_t) * (5 * static_cast<size_t>(cfg->max_seqs) + 2), 256) +
+    // Multi-query units: at most (tokens/16 + sequences) tiles per kv head.
+    const size_t max_units =
+        (static_cast<size_t>(cfg->max_step_tokens) / kva::kMqRows + cfg->max_seqs) * cfg->num_kv_heads;
+    c->step_bytes = round_up(sizeof(int32_t) * (6 * static_cast<size_t>(cfg->max_seqs) + 3), 256) +
+                    round_up(sizeof(int32_t) * (max_units + 1), 256) +
                     round_up(sizeof(int32_t) * 3 * static_cast<size_t>(cfg->max_step_tokens), 256) +
                     round_up(sizeof(uint64_t) * static_cast<size_t>(cfg->max_step_tokens), 256) + 1024;
     const size_t patch_cap = std::max<size_t>(4096, cfg->max_seqs + cfg->max_step_tokens);
@@ -316,6 +326,13 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
             return cleanup(hip_fail(e, "hipMalloc(workspace)"));
         if ((e = hipMalloc(&c->d_ws_ml, units * 2 * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(workspace ml)"));
+        // Multi-query partial slots: two per workgroup, one workgroup per CU.
+        c->mq_max_wg = c->n_cu;
+        const size_t mq_rows = static_cast<size_t>(2) * c->mq_max_wg * kMaxGroup * kva::kMqRows;
+        if ((e = hipMalloc(&c->d_mq_acc, mq_rows * kva::kHeadDim * sizeof(float))) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMalloc(multi-query workspace)"));
+        if ((e = hipMalloc(&c->d_mq_ml, mq_rows * 2 * sizeof(float))) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMalloc(multi-query workspace ml)"));
         for (int i = 0; i < kStageSlots; ++i) {
             if ((e = hipHostMalloc(reinterpret_cast<void **>(&c->h_stage[i]), c->stage_bytes,
                                    hipHostMallocDefault)) != hipSuccess)
@@ -344,6 +361,8 @@ int kva_destroy(kva_cache *c) {
         (void)hipFree(c->d_aux);
         (void)hipFree(c->d_ws_acc);
         (void)hipFree(c->d_ws_ml);
+        (void)hipFree(c->d_mq_acc);
+        (void)hipFree(c->d_mq_ml);
     }
     delete c;
     return KVA_OK;
@@ -551,7 +570,12 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     const size_t o_start = o_ctx + sizeof(int32_t) * n_seqs;
     const size_t o_tokoff = o_start + sizeof(int32_t) * n_seqs;
     const size_t o_pre = o_tokoff + sizeof(int32_t) * (n_seqs + 1);
-    const size_t o_tseq = round_up(o_pre + sizeof(int32_t) * (n_seqs + 1), 16);
+    int64_t n_units = 0;
+    for (int32_t b = 0; b < n_seqs; ++b)
+        n_units += static_cast<int64_t>((n_new[b] + kva::kMqRows - 1) / kva::kMqRows) * c->cfg.num_kv_heads;
+    const size_t o_upre = o_pre + sizeof(int32_t) * (n_seqs + 1);
+    const size_t o_mqpre = o_upre + sizeof(int32_t) * (n_seqs + 1);
+    const size_t o_tseq = round_up(o_mqpre + sizeof(int32_t) * (n_units + 1), 16);
     const size_t o_tslot = round_up(o_tseq + sizeof(int32_t) * n_tok, 16);
     const size_t o_tpos = round_up(o_tslot + sizeof(int32_t) * n_tok, 16);
     const size_t o_bits = round_up(o_tpos + sizeof(int32_t) * n_tok, 16);
@@ -597,6 +621,26 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     }
     p_off[n_seqs] = t;
     p_pre[n_seqs] = static_cast<int32_t>(pages);
+    // Multi-query units in (sequence, tile, kv head) order with their key
+    // blocks: a tree tile reads the whole cache, a causal tile reads up to
+    // its last token's slot.
+    int32_t *p_upre = at<int32_t>(h, o_upre), *p_mqpre = at<int32_t>(h, o_mqpre);
+    int64_t units = 0, blocks = 0;
+    for (int32_t b = 0; b < n_seqs; ++b) {
+        p_upre[b] = static_cast<int32_t>(units);
+        const int32_t tiles = (n_new[b] + kva::kMqRows - 1) / kva::kMqRows;
+        for (int32_t tl = 0; tl < tiles; ++tl) {
+            const int64_t keys = tree_bits ? p_ctx[b]
+                                           : p_start[b] + std::min(n_new[b], (tl + 1) * kva::kMqRows);
+            const int64_t nb = (keys + kva::kMqKeys - 1) / kva::kMqKeys;
+            for (int32_t hh = 0; hh < c->cfg.num_kv_heads; ++hh) {
+                p_mqpre[units++] = static_cast<int32_t>(blocks);
+                blocks += nb;
+            }
+        }
+    }
+    p_upre[n_seqs] = static_cast<int32_t>(units);
+    p_mqpre[units] = static_cast<int32_t>(blocks);
     if (tree_bits) std::memcpy(h + o_bits, tree_bits, sizeof(uint64_t) * n_tok);
 
     if (!c->host_only) {
@@ -623,6 +667,10 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->st_max_new = max_new;
     c->st_max_pos = max_pos;
     c->st_total_pages = static_cast<int32_t>(pages);
+    c->st_mq_units = static_cast<int32_t>(units);
+    c->st_mq_blocks = static_cast<int32_t>(blocks);
+    c->off_upre = o_upre;
+    c->off_mqpre = o_mqpre;
     c->st_all_one = all_one;
     c->st_has_bits = tree_bits != nullptr;
     c->step_valid = true;
@@ -746,11 +794,19 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     a.new_start = at<int32_t>(c->d_step, c->off_start);
     a.tok_off = at<int32_t>(c->d_step, c->off_tokoff);
     a.tok_bits = tree ? at<uint64_t>(c->d_step, c->off_bits) : nullptr;
+    a.upre = at<int32_t>(c->d_step, c->off_upre);
+    a.mq_pre = at<int32_t>(c->d_step, c->off_mqpre);
     a.n_seqs = c->st_n_seqs;
-    a.max_new = c->st_max_new;
+    a.n_units = c->st_mq_units;
+    a.total_blocks = c->st_mq_blocks;
+    // Stream-K share: one workgroup per CU, at least 4 key blocks each.
+    a.n_wg = static_cast<int32_t>(
+        std::max<int64_t>(1, std::min<int64_t>(c->mq_max_wg, (c->st_mq_blocks + 3) / 4)));
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
     a.tree = tree ? 1 : 0;
+    a.ws_acc = c->d_mq_acc;
+    a.ws_ml = c->d_mq_ml;
     const hipError_t e = kva::launch_multi_query(a, static_cast<hipStream_t>(stream));
     if (e == hipErrorNotSupported)
         return fail(KVA_ERR_UNSUPPORTED, "multi-query attention kernel not available for this shape");

@@ -114,12 +114,20 @@ struct MultiQueryArgs {
     const int32_t *new_start; // device [n_seqs]: first new slot
     const int32_t *tok_off;   // device [n_seqs+1]: new-token ranges
     const uint64_t *tok_bits; // device [T] (tree mode) or null
+    const int32_t *upre;      // device [n_seqs+1]: units of earlier sequences
+    const int32_t *mq_pre;    // device [n_units+1]: key blocks of earlier units
     int32_t n_seqs;
-    int32_t max_new;          // most new tokens of one sequence
+    int32_t n_units;          // (sequence, 16-token tile, kv head) units
+    int32_t total_blocks;     // key blocks of all units
+    int32_t n_wg;             // workgroups sharing the blocks (stream-K)
     int32_t num_heads;
     int32_t num_kv_heads;
     int32_t tree;             // 0 = causal chunk, 1 = tree mask
+    float *ws_acc;            // [2*n_wg][G][16][256] partial slots
+    float *ws_ml;             // [2*n_wg][G][16][2]
 };
+constexpr int kMqKeys = 32;   // keys per multi-query block
+constexpr int kMqRows = 16;   // query tokens per unit tile
 hipError_t launch_multi_query(const MultiQueryArgs &a, hipStream_t s);
 
 }  // namespace kva
