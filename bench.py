@@ -175,6 +175,126 @@ def c2_workload(dev, steps_unused, warmup):
     return {"wall_s": wall, "steps": n_steps, "kv_bytes": kv}
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
+
+
+def c4_workload(dev, steps, warmup):
+    """Config 4: 4 sequences append a 512-token chunk after 0/256/1024/2048
+    cached rows (fused norm+RoPE+append), then causal prefill attention; 16
+    layers per step.  Lengths are set back after each step."""
+    prefix, chunk = list(wl.C4_PREFIX), [wl.C4_CHUNK] * 4
+    B, T = 4, sum(chunk)
+    nblk = [(p + c + 15) // 16 for p, c in zip(prefix, chunk)]
+    cache = PagedKVCache(n_layers=LAYERS, max_seqs=B, max_blocks=sum(nblk), max_blocks_per_seq=max(nblk),
+                         max_step_tokens=T)
+    perm = np.random.default_rng(0).permutation(sum(nblk))
+    o = 0
+    for b, n in enumerate(nblk):
+        cache.set_blocks(b, [int(x) for x in perm[o:o + n]])
+        o += n
+    cache.sync_tables()
+    fill_pools(dev, cache, sum(nblk))
+    cos, sin = rope_tables(4096)
+    d_cos, d_sin = dev.array(cos), dev.array(sin)
+    inputs = make_inputs(dev, T)
+    seqs = list(range(B))
+
+    def step(evs=None):
+        for b in seqs:
+            cache.set_len(b, prefix[b])
+        cache.begin_step(seqs, chunk)
+        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
+            if evs is not None:
+                evs[layer][0].record()
+            cache.prefill(layer, q, out)
+            if evs is not None:
+                evs[layer][1].record()
+
+    for _ in range(warmup):
+        step()
+    dev.synchronize()
+    evs = [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s]
+    cache.destroy()
+    flops = 4 * H * D * sum(sum(p + i + 1 for i in range(c)) for p, c in zip(prefix, chunk))
+    by = (sum(p + c for p, c in zip(prefix, chunk)) * ROW_BYTES + 2 * T * H * D * 2)
+    return {"wall_s": wall, "steps": steps, "tokens": T, "flops_per_layer": flops, "bytes_per_layer": by,
+            "prefill_avg_us": float(np.mean(ms) * 1e3)}
+
+
+def c5_workload(dev, steps, warmup, layers=4, batch=64):
+    """Config 5: 64 sequences with cached lengths U[4096, 32768] (seed 0)
+    append the 9-node draft tree (RoPE at len+depth), run tree-verify
+    attention, then keep a seeded root-to-node path and roll back the rest
+    (all layers).  `layers` full-attention layers per step (the pools of 16
+    layers would hold 77 GB; per-layer figures are what is reported)."""
+    from mi50grad_amd import tree as tr
+
+    spec = wl.c5_spec(0, batch=batch)
+    lengths = [int(x) for x in spec.lengths]
+    T = 9 * batch
+    cache = PagedKVCache(n_layers=layers, max_seqs=batch, max_blocks=spec.n_blocks,
+                         max_blocks_per_seq=max(len(i) for i in spec.block_ids), max_step_tokens=T)
+    for b, ids in enumerate(spec.block_ids):
+        cache.set_blocks(b, ids)
+    cache.sync_tables()
+    fill_pools(dev, cache, spec.n_blocks)
+    rows = max(lengths) + 16
+    cos, sin = rope_tables(rows)
+    d_cos, d_sin = dev.array(cos), dev.array(sin)
+    rng = np.random.default_rng(1)
+    inputs = [tuple(dev.array(x) for x in (wl.normal_f16(rng, (T, H, D)), wl.normal_f16(rng, (T, HKV, D)),
+                                          wl.normal_f16(rng, (T, HKV, D)), wl.norm_weight(rng),
+                                          wl.norm_weight(rng))) + (dev.empty((T, H, D), np.float16),)
+              for _ in range(layers)]
+    depth = tr.depths(wl.C5_PARENTS)
+    rope_pos = [L + d for L in lengths for d in depth]
+    bits = tr.tree_bits(wl.C5_PARENTS) * batch
+    accept = np.random.default_rng(2).integers(0, 9, batch)
+    keep = [tr.root_to_node_path(wl.C5_PARENTS, int(n)) for n in accept]
+    seqs = list(range(batch))
+
+    def step(evs=None):
+        for b in seqs:
+            cache.set_len(b, lengths[b])
+        cache.begin_step(seqs, [9] * batch, rope_pos=rope_pos, tree_bits=bits)
+        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
+            if evs is not None:
+                evs[layer][0].record()
+            cache.tree_verify(layer, q, out)
+            if evs is not None:
+                evs[layer][1].record()
+        if evs is not None:
+            evs[layers][0].record()
+        cache.rollback(seqs, lengths, keep)
+        if evs is not None:
+            evs[layers][1].record()
+
+    for _ in range(warmup):
+        step()
+    dev.synchronize()
+    evs = [[[Event(), Event()] for _ in range(layers + 1)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    verify_ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s[:layers]]
+    rb_ms = [s[layers][0].elapsed_ms(s[layers][1]) for s in evs]
+    cache.destroy()
+    kv = sum(lengths) * ROW_BYTES + T * ROW_BYTES
+    return {"wall_s": wall, "steps": steps, "layers": layers, "kv_bytes_per_layer": kv,
+            "alg_bytes_per_layer": kv + 2 * T * H * D * 2, "verify_avg_us": float(np.mean(verify_ms) * 1e3),
+            "rollback_avg_us": float(np.mean(rb_ms) * 1e3), "sum_len": sum(lengths)}
+
+
 def copy_probe(dev, gib: float = 4.0, reps: int = 20):
     n = int(gib * (1 << 30)) // 16 * 16
     a, b = dev.malloc(n), dev.malloc(n)
@@ -238,7 +358,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "copy"])
+    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "c4", "c5", "copy"])
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -264,6 +384,37 @@ def main() -> int:
                           "data": "synthetic", "config": {"workload": "C2"}}))
         return 0
 
+    if args.workload == "c4":
+        r = c4_workload(dev, args.steps, args.warmup)
+        tflops = r["flops_per_layer"] / (r["prefill_avg_us"] * 1e-6) / 1e12
+        ms = r["wall_s"] * 1e3 / r["steps"]
+        print(json.dumps({
+            "metric": "config-4 chunked prefill attention TFLOP/s (pp512 after 0/256/1024/2048 rows, B=4)",
+            "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
+            "config": {"workload": "C4", "layers": LAYERS, "tokens_per_step": r["tokens"]},
+            "tok_per_s": r["tokens"] * r["steps"] / r["wall_s"],
+            "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": None,
+                         "kernel": "kva_prefill = mq_kernel<6> + mq_combine_kernel<6>",
+                         "avg_us": r["prefill_avg_us"], "alg_flops_per_launch": r["flops_per_layer"],
+                         "alg_bytes_per_launch": r["bytes_per_layer"]}}))
+        return 0
+    if args.workload == "c5":
+        r = c5_workload(dev, args.steps, args.warmup)
+        gbs = r["alg_bytes_per_layer"] / (r["verify_avg_us"] * 1e-6) / 1e9
+        ms = r["wall_s"] * 1e3 / r["steps"]
+        print(json.dumps({
+            "metric": "config-5 tree-verify attention GB/s (B=64, ctx U[4096,32768], 9-node tree)",
+            "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
+            "config": {"workload": "C5", "layers": r["layers"], "sum_len": r["sum_len"]},
+            "rollback_avg_us": r["rollback_avg_us"],
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                         "kernel": "kva_tree_verify = mq_kernel<6> + mq_combine_kernel<6>",
+                         "avg_us": r["verify_avg_us"], "alg_bytes_per_launch": r["alg_bytes_per_layer"]}}))
+        return 0
     if args.workload == "c3":
         spec = wl.c3_spec(0)
         lengths, ids, nb = spec.lengths, spec.block_ids, spec.n_blocks

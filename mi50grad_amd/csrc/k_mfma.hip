@@ -53,33 +53,65 @@ __device__ __forceinline__ int upper_index(const int32_t *pre, int n, int x) {
     return lo;
 }
 
-// Staged chunks of one 32-key block: K and V rows, 16 bytes per chunk;
-// 1024 chunks each, spread over the workgroup's threads.
+// Staged 32-key block.  K: 1024 chunks of 16 bytes (key = c/32, dims
+// 8*(c%32)..+8) spread over the threads.  V: 256 tasks of 4 keys x 8 dims
+// (keys 4*(v/32).., dims 8*(v%32)..), transposed in registers so each dim's
+// 4 keys are stored to V^T with one 8-byte write.
 template <int NT>
 struct Stage {
-    static constexpr int kPer = (kMqKeys * kHeadDim / 8 + NT - 1) / NT;
-    uint4 k[kPer];
-    uint4 v[kPer];
+    static constexpr int kPerK = (kMqKeys * 32 + NT - 1) / NT;
+    static constexpr int kPerV = (kMqKeys / 4 * 32 + NT - 1) / NT;
+    uint4 k[kPerK];
+    uint4 v[kPerV][4];
 };
 
+// Page ids of a block's two 16-key pages (wave-uniform scalars).
+struct BlockPages {
+    int p0, p1;
+};
+
+__device__ __forceinline__ BlockPages block_pages(const int32_t *trow, int blk, int ctx) {
+    const int pg = 2 * blk;
+    BlockPages bp;
+    bp.p0 = __builtin_amdgcn_readfirstlane(trow[pg]);
+    bp.p1 = (pg + 1) * kBlockTokens < ctx ? __builtin_amdgcn_readfirstlane(trow[pg + 1]) : bp.p0;
+    return bp;
+}
+
 template <int NT>
-__device__ __forceinline__ void stage_load(Stage<NT> &st, const MultiQueryArgs &a,
-                                           const int32_t *trow, int h, int key0, int ctx) {
+__device__ __forceinline__ void stage_load(Stage<NT> &st, const MultiQueryArgs &a, BlockPages bp,
+                                           int h, int key0, int ctx) {
     const int tid = threadIdx.x;
     const size_t row_elems = static_cast<size_t>(a.num_kv_heads) * kHeadDim;
+    const size_t head_off = static_cast<size_t>(h) * kHeadDim;
 #pragma unroll
-    for (int i = 0; i < Stage<NT>::kPer; ++i) {
+    for (int i = 0; i < Stage<NT>::kPerK; ++i) {
         const int c = tid + i * NT;
-        const int key = key0 + (c >> 5);
-        const int col = (c & 31) * 8;
-        if (c < kMqKeys * 32 && key < ctx) {
-            const size_t off = (static_cast<size_t>(trow[key >> 4]) * kBlockTokens + (key & 15)) * row_elems +
-                               static_cast<size_t>(h) * kHeadDim + col;
+        const int kk = c >> 5;
+        if (c < kMqKeys * 32 && key0 + kk < ctx) {
+            const int page = kk < 16 ? bp.p0 : bp.p1;
+            const size_t off = (static_cast<size_t>(page) * kBlockTokens + (kk & 15)) * row_elems + head_off +
+                               (c & 31) * 8;
             st.k[i] = ld16(a.k_pool + off);
-            st.v[i] = ld16(a.v_pool + off);
         } else {
             st.k[i] = make_uint4(0, 0, 0, 0);
-            st.v[i] = make_uint4(0, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < Stage<NT>::kPerV; ++i) {
+        const int v = tid + i * NT;
+        const int kg = v >> 5;
+        const int col = (v & 31) * 8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int kk = 4 * kg + e;
+            if (v < kMqKeys / 4 * 32 && key0 + kk < ctx) {
+                const int page = kk < 16 ? bp.p0 : bp.p1;
+                st.v[i][e] = ld16(a.v_pool + (static_cast<size_t>(page) * kBlockTokens + (kk & 15)) * row_elems +
+                                  head_off + col);
+            } else {
+                st.v[i][e] = make_uint4(0, 0, 0, 0);
+            }
         }
     }
 }
@@ -88,17 +120,31 @@ template <int NT>
 __device__ __forceinline__ void stage_store(const Stage<NT> &st, uint16_t *k_lds, uint16_t *vt_lds) {
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < Stage<NT>::kPer; ++i) {
+    for (int i = 0; i < Stage<NT>::kPerK; ++i) {
         const int c = tid + i * NT;
-        if (c < kMqKeys * 32) {
-            const int key = c >> 5;
-            const int col = (c & 31) * 8;
-            *reinterpret_cast<uint4 *>(k_lds + key * kKRow + col) = st.k[i];
-            const uint32_t vw[4] = {st.v[i].x, st.v[i].y, st.v[i].z, st.v[i].w};
+        if (c < kMqKeys * 32)
+            *reinterpret_cast<uint4 *>(k_lds + (c >> 5) * kKRow + (c & 31) * 8) = st.k[i];
+    }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vt_lds[(col + 2 * e) * kVRow + key] = static_cast<uint16_t>(vw[e] & 0xffffu);
-                vt_lds[(col + 2 * e + 1) * kVRow + key] = static_cast<uint16_t>(vw[e] >> 16);
+    for (int i = 0; i < Stage<NT>::kPerV; ++i) {
+        const int v = tid + i * NT;
+        if (v < kMqKeys / 4 * 32) {
+            const int key = 4 * (v >> 5);
+            const int col = (v & 31) * 8;
+            // word w of key e holds dims col+2w, col+2w+1
+            const uint32_t w0[4] = {st.v[i][0].x, st.v[i][0].y, st.v[i][0].z, st.v[i][0].w};
+            const uint32_t w1[4] = {st.v[i][1].x, st.v[i][1].y, st.v[i][1].z, st.v[i][1].w};
+            const uint32_t w2[4] = {st.v[i][2].x, st.v[i][2].y, st.v[i][2].z, st.v[i][2].w};
+            const uint32_t w3[4] = {st.v[i][3].x, st.v[i][3].y, st.v[i][3].z, st.v[i][3].w};
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint2 lo, hi;  // dims col+2w (low halves) and col+2w+1 (high halves), keys key..key+3
+                lo.x = (w0[w] & 0xffffu) | (w1[w] << 16);
+                lo.y = (w2[w] & 0xffffu) | (w3[w] << 16);
+                hi.x = (w0[w] >> 16) | (w1[w] & 0xffff0000u);
+                hi.y = (w2[w] >> 16) | (w3[w] & 0xffff0000u);
+                *reinterpret_cast<uint2 *>(vt_lds + (col + 2 * w) * kVRow + key) = lo;
+                *reinterpret_cast<uint2 *>(vt_lds + (col + 2 * w + 1) * kVRow + key) = hi;
             }
         }
     }
@@ -165,15 +211,21 @@ __global__ __launch_bounds__(64 * G) void mq_kernel(MultiQueryArgs a) {
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) acc[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+        // Pipeline: block blk+1's K/V loads and block blk+2's page ids are in
+        // flight while block blk is computed from LDS.
         Stage<NT> stg;
         const int blk0 = p - ub;
         const int blk1 = seg_end - ub;
-        stage_load<NT>(stg, a, trow, h, blk0 * kMqKeys, ctx);
+        stage_load<NT>(stg, a, block_pages(trow, blk0, ctx), h, blk0 * kMqKeys, ctx);
+        BlockPages nxt = block_pages(trow, blk0 + 1 < blk1 ? blk0 + 1 : blk0, ctx);
         for (int blk = blk0; blk < blk1; ++blk) {
             __syncthreads();  // previous block's LDS reads are done
             stage_store<NT>(stg, k_lds, vt_lds);
             __syncthreads();
-            if (blk + 1 < blk1) stage_load<NT>(stg, a, trow, h, (blk + 1) * kMqKeys, ctx);
+            if (blk + 1 < blk1) {
+                stage_load<NT>(stg, a, nxt, h, (blk + 1) * kMqKeys, ctx);
+                nxt = block_pages(trow, blk + 2 < blk1 ? blk + 2 : blk + 1, ctx);
+            }
             const int key0 = blk * kMqKeys;
 
             // S^T for keys key0 + 16*nt + 4*grp + i, query column `col`.
