@@ -186,7 +186,7 @@ int kva_rollback(kva_cache *cache, int32_t n_seqs, const int32_t *seq_ids,
                  const int32_t *base_len, const int32_t *keep_off,
                  const int32_t *keep_rows, kva_stream_t stream);
 
-/* Split-K tuning for kva_decode: tokens per split (multiple of 64); 0 =
+/* Split-K tuning for kva_decode: tokens per split (multiple of 16); 0 =
  * automatic.  Returns the value in effect through *effective.             */
 int kva_set_decode_split(kva_cache *cache, int32_t split_tokens);
 int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,

@@ -76,6 +76,15 @@ __device__ __forceinline__ float wave_groups_sum(float x) {
     return x;
 }
 
+// Wave-uniform read of read-only metadata (block-table entries, plans)
+// through the scalar cache: a load in the constant address space with a
+// uniform address becomes a scalar load, counted apart from the vector
+// loads, so waiting for it does not also wait for K/V data in flight.
+__device__ __forceinline__ int32_t ld_uniform(const int32_t *p) {
+    return *reinterpret_cast<const __attribute__((address_space(4))) int32_t *>(
+        reinterpret_cast<uintptr_t>(p));
+}
+
 __device__ __forceinline__ uint4 ld16(const uint16_t *p) {
     return *reinterpret_cast<const uint4 *>(p);
 }

@@ -5,27 +5,29 @@
 // (:222) — generalised to a batch of sequences with ragged lengths read
 // through a block table, and to any number of KV splits.
 //
-// Work split: stream-K over pages (see decode_kernel).  A 256-thread
-// workgroup processes (sequence, kv head) unit segments; the G = H/Hkv query
-// heads of the KV head share every K/V byte it loads (the reference re-read
-// each KV head G times, once per query head).  The four waves take
-// interleaved 16-token pages of a segment, each with its own online-softmax
-// state, and merge through LDS at the segment's end.
+// Work split: stream-K over pages (see decode_kernel).  A workgroup holds two
+// waves per kv head; both walk the same pages, wave k taking tokens
+// 8k..8k+7 of every 16-token page, and merge through LDS when a sequence
+// ends.  The G = H/Hkv query heads of a KV head share every K/V byte its
+// waves load (the reference re-read each KV head G times, once per query
+// head).  Two waves per SIMD hide each other's load waits and issue turns.
 //
-// Per page, per wave (lane = 16*r + j):
-//   loads: the next page's K is prefetched into the second of two register
-//       buffers (ping-pong) and the current page's V is issued before QK, so
-//       every wave keeps 8-16 KB in flight during its arithmetic;
-//   QK: the 16 lanes of row r hold tokens r, r+4, r+8, r+12, 16 dims each
+// Per page half, per wave (lane = 16*r + j):
+//   loads: a ring of three register buffers; while one half page is folded
+//       in, the next two pages' halves (16 KB per wave) are in flight, across
+//       sequence boundaries too.  Buffer loads through a per-page resource: its range
+//       check zero-fills rows past a sequence's end and turns a prefetch past
+//       the range into a no-op that still counts;
+//   QK: the 16 lanes of row r hold tokens 8k+r and 8k+r+4, 16 dims each
 //       (16-byte pieces j and j+16 of the 512-byte row: each load is 256
-//       contiguous bytes per token), dot with the G query heads via
-//       v_dot2_f32_f16; a 16-lane DPP sum finishes each score;
-//   softmax: log2 domain; page max over the four rows with row-broadcast
-//       DPP and one v_readlane (no LDS round trips); v_exp_f32;
-//       probabilities rounded to fp16 pairs;
+//       contiguous bytes per token), dot with the G query rows (held in
+//       registers) via v_dot2_f32_f16; a 16-lane DPP sum finishes each score;
+//   softmax: log2 domain; max over the four rows with row-broadcast DPP and
+//       one v_readlane (no LDS round trips); v_exp_f32; probabilities
+//       rounded to fp16 pairs;
 //   PV: lane owns dims 4*lane..4*lane+3 of all G heads; tokens t and t+4
 //       are paired so one v_dot2_f32_f16 folds two tokens; the pair's
-//       probabilities come from row t%4 via v_readlane (wave-uniform).
+//       probabilities (row t's) reach every lane by an LDS broadcast.
 #include "k_common.h"
 #include "kva_internal.h"
 
@@ -43,57 +45,95 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
-struct KRegs {
-    uint4 k[4][2];  // tokens r + 4*t4, pieces j and j+16
-};
-struct VRegs {
-    uint2 v[16];    // all 16 tokens, dims 4*lane..4*lane+3
+constexpr int kHalf = kBlockTokens / 2;  // tokens per wave per page
+
+// One wave's half page: K tokens 8k + r + 4*t4 (t4 = 0, 1), pieces j and
+// j+16; V tokens 8k + t (t = 0..7), dims 4*lane..4*lane+3.
+struct HalfPage {
+    uint4 k[2][2];
+    uint2 v[kHalf];
 };
 
-// Load a page's K (row stride row_bytes) into registers; rows >= lim read as 0.
-template <bool kFull>
-__device__ __forceinline__ void load_k(KRegs &p, const char *kb, uint32_t koff, int row_bytes,
-                                       int r, int lim) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const char *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(base), 0, bytes, 0x00020000);
+}
+
+// Load a half page (kb, vb: the page's first row, this head's 512 bytes;
+// koff/voff already hold this wave's first row).  Full (or disabled) pages
+// carry the row offset in soffset; a partial page puts it in voffset so the
+// range check (num_records = valid rows * row_bytes) returns zeros for the
+// rows past the sequence's end without touching memory, and a disabled page
+// (num_records = 0) fetches nothing.  Both forms issue the same loads, so the
+// compiler's load counters stay exact across the branch.
+__device__ __forceinline__ void load_half(HalfPage &p, const char *kb, const char *vb, int lim, bool on,
+                                          uint32_t koff, uint32_t voff, int row_bytes) {
+    if (!on || lim >= kBlockTokens) {
+        const uint32_t n = on ? 0x7fffffffu : 0u;
+        const auto rk = page_rsrc(kb, n), rv = page_rsrc(vb, n);
 #pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4) {
-        const char *base = kb + t4 * 4 * row_bytes + koff;
-        if (kFull || r + 4 * t4 < lim) {
-            p.k[t4][0] = *reinterpret_cast<const uint4 *>(base);
-            p.k[t4][1] = *reinterpret_cast<const uint4 *>(base + 256);
-        } else {
-            p.k[t4][0] = make_uint4(0, 0, 0, 0);
-            p.k[t4][1] = make_uint4(0, 0, 0, 0);
+        for (int t4 = 0; t4 < 2; ++t4)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const auto x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 256 * q, t4 * 4 * row_bytes, 0);
+                p.k[t4][q] = make_uint4(x[0], x[1], x[2], x[3]);
+            }
+#pragma unroll
+        for (int t = 0; t < kHalf; ++t) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, t * row_bytes, 0);
+            p.v[t] = make_uint2(x[0], x[1]);
+        }
+    } else {
+        const uint32_t n = static_cast<uint32_t>(lim * row_bytes);
+        const auto rk = page_rsrc(kb, n), rv = page_rsrc(vb, n);
+#pragma unroll
+        for (int t4 = 0; t4 < 2; ++t4)
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const auto x =
+                    __builtin_amdgcn_raw_buffer_load_b128(rk, koff + t4 * 4 * row_bytes + 256 * q, 0, 0);
+                p.k[t4][q] = make_uint4(x[0], x[1], x[2], x[3]);
+            }
+#pragma unroll
+        for (int t = 0; t < kHalf; ++t) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + t * row_bytes, 0, 0);
+            p.v[t] = make_uint2(x[0], x[1]);
         }
     }
 }
 
-template <bool kFull>
-__device__ __forceinline__ void load_v(VRegs &p, const char *vb, uint32_t voff, int row_bytes,
-                                       int lim) {
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-        if (kFull || t < lim)
-            p.v[t] = *reinterpret_cast<const uint2 *>(vb + t * row_bytes + voff);
-        else
-            p.v[t] = make_uint2(0, 0);
-    }
-}
-
+// m is the running max of the raw scores q.k; probabilities are
+// exp2((s - m) * log2(e)/16).
 template <int G>
 struct WaveState {
     float m[G], l[G], acc[G][4];
 };
 
-// Fold one page into the wave's online-softmax state.  lim < 16 masks rows.
-template <int G, bool kFull>
-__device__ __forceinline__ void compute_page(WaveState<G> &st, const KRegs &p, const VRegs &pv,
-                                             const uint4 (&qv)[G][2], int r, int lim) {
+template <int G>
+__device__ __forceinline__ void reset(WaveState<G> &st) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        st.m[g] = -INFINITY;
+        st.l[g] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) st.acc[g][c] = 0.0f;
+    }
+}
+
+// Fold a half page into the wave's online-softmax state; tokens r + 4*t4 >=
+// lim (relative to the half) are masked, lim >= 1.  qv: this lane's 16-byte
+// pieces j and j+16 of the G query rows.  pbuf: this wave's 32 dwords of LDS
+// through which PV's probability pairs are broadcast: a v_readlane per pair
+// and head would cost a VALU issue plus a dependent-SGPR stall each.
+template <int G>
+__device__ __forceinline__ void compute_half(WaveState<G> &st, const HalfPage &p, const uint4 (&qv)[G][2],
+                                             int r, int j, int lim, uint32_t *pbuf) {
     const float qk_scale = kLog2e / 16.0f;  // log2(e) / sqrt(256)
-    float s[G][4];
+    const uint32_t kOnes = 0x3c003c00u;     // fp16 pair (1, 1)
+    float s[G][2];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) {
 #pragma unroll
-        for (int t4 = 0; t4 < 4; ++t4) {
+        for (int t4 = 0; t4 < 2; ++t4) {
             float x = 0.0f;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
@@ -102,57 +142,77 @@ __device__ __forceinline__ void compute_page(WaveState<G> &st, const KRegs &p, c
                 x = dot2(qv[g][q].z, p.k[t4][q].z, x);
                 x = dot2(qv[g][q].w, p.k[t4][q].w, x);
             }
-            s[g][t4] = row16_sum(x) * qk_scale;
+            s[g][t4] = row16_sum(x);
         }
-    if (!kFull) {
+    }
+    if (lim < kHalf) {  // the sequence's last page (wave-uniform)
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int t4 = 0; t4 < 4; ++t4) s[g][t4] = (r + 4 * t4 < lim) ? s[g][t4] : -INFINITY;
+            for (int t4 = 0; t4 < 2; ++t4) s[g][t4] = (r + 4 * t4 < lim) ? s[g][t4] : -INFINITY;
     }
-    // Page max per head: the 16 lanes of a row agree, so a row-broadcast DPP
-    // max (rows 1,3 <- rows 0,2; then rows 2,3 <- row 1) leaves the wave max
-    // in lane 63; all heads are reduced together to overlap the DPP hazards.
+    // Max per head: the 16 lanes of a row agree, so a row-broadcast DPP max
+    // (rows 1,3 <- rows 0,2; then rows 2,3 <- row 1) leaves the wave max in
+    // lane 63; all heads are reduced together to overlap the DPP hazards.
     float bm[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) bm[g] = fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3]));
+    for (int g = 0; g < G; ++g) bm[g] = fmaxf(s[g][0], s[g][1]);
 #pragma unroll
     for (int g = 0; g < G; ++g) bm[g] = fmaxf(bm[g], dpp_masked_f<kDppRowBcast15, 0xA>(bm[g]));
 #pragma unroll
     for (int g = 0; g < G; ++g) bm[g] = fmaxf(bm[g], dpp_masked_f<kDppRowBcast31, 0xC>(bm[g]));
-    uint32_t pa[G], pb[G];  // fp16 pairs: tokens (r, r+4) and (r+8, r+12)
+    float mn[G];
+    bool grew = false;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const float mn = fmaxf(st.m[g], __builtin_bit_cast(float, __builtin_amdgcn_readlane(
-                                                                __builtin_bit_cast(int, bm[g]), 63)));
-        const float corr = __builtin_amdgcn_exp2f(st.m[g] - mn);
-        pa[g] = pack_h2(__builtin_amdgcn_exp2f(s[g][0] - mn), __builtin_amdgcn_exp2f(s[g][1] - mn));
-        pb[g] = pack_h2(__builtin_amdgcn_exp2f(s[g][2] - mn), __builtin_amdgcn_exp2f(s[g][3] - mn));
-        st.l[g] = st.l[g] * corr + ((lo_f(pa[g]) + hi_f(pa[g])) + (lo_f(pb[g]) + hi_f(pb[g])));
-        st.m[g] = mn;
+        mn[g] = fmaxf(st.m[g], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bm[g]), 63)));
+        grew = grew || mn[g] > st.m[g];
+    }
+    // Rescale l and acc only when some head's max grew (wave-uniform test):
+    // after the first pages of a sequence the max rarely moves.
+    if (grew) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) st.acc[g][c] *= corr;
+        for (int g = 0; g < G; ++g) {
+            const float corr = __builtin_amdgcn_exp2f((st.m[g] - mn[g]) * qk_scale);
+            st.l[g] *= corr;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) st.acc[g][c] *= corr;
+            st.m[g] = mn[g];
+        }
+    }
+    uint32_t pa[G];  // fp16 pair: tokens r and r+4 of the half
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float off = -mn[g] * qk_scale;
+        pa[g] = pack_h2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[g][0], qk_scale, off)),
+                        __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][1], qk_scale, off)));
+        st.l[g] = dot2(pa[g], kOnes, st.l[g]);  // l sums the fp16 probabilities PV uses
+    }
+    // Row r's pairs (the same in all 16 lanes of the row) to pbuf[8r + g];
+    // every lane then reads each row's pairs back as one broadcast. The
+    // wave's LDS operations run in order, so the previous half page's reads
+    // are done before these writes land.
+    if (j == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) pbuf[8 * r + g] = pa[g];
     }
 #pragma unroll
-    for (int pr = 0; pr < 8; ++pr) {
-        // Pair pr: row rr = pr & 3, tokens (rr, rr+4) or (rr+8, rr+12).
-        const int rr = pr & 3;
-        const int t0 = rr + (pr >> 2) * 8;
-        const uint2 va = pv.v[t0];
-        const uint2 vb = pv.v[t0 + 4];
+    for (int rr = 0; rr < 4; ++rr) {
+        uint32_t pp[8];
+        *reinterpret_cast<uint4 *>(pp) = reinterpret_cast<const uint4 *>(pbuf)[2 * rr];
+        if (G > 4) *reinterpret_cast<uint4 *>(pp + 4) = reinterpret_cast<const uint4 *>(pbuf)[2 * rr + 1];
+        const uint2 va = p.v[rr];
+        const uint2 vb = p.v[rr + 4];
         const uint32_t v0 = (va.x & 0xffffu) | (vb.x << 16);
         const uint32_t v1 = (va.x >> 16) | (vb.x & 0xffff0000u);
         const uint32_t v2 = (va.y & 0xffffu) | (vb.y << 16);
         const uint32_t v3 = (va.y >> 16) | (vb.y & 0xffff0000u);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const uint32_t src = (pr >> 2) ? pb[g] : pa[g];
-            const uint32_t pp =
-                static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(src), rr * 16));
-            st.acc[g][0] = dot2(pp, v0, st.acc[g][0]);
-            st.acc[g][1] = dot2(pp, v1, st.acc[g][1]);
-            st.acc[g][2] = dot2(pp, v2, st.acc[g][2]);
-            st.acc[g][3] = dot2(pp, v3, st.acc[g][3]);
+            st.acc[g][0] = dot2(pp[g], v0, st.acc[g][0]);
+            st.acc[g][1] = dot2(pp[g], v1, st.acc[g][1]);
+            st.acc[g][2] = dot2(pp[g], v2, st.acc[g][2]);
+            st.acc[g][3] = dot2(pp[g], v3, st.acc[g][3]);
         }
     }
 }
@@ -169,20 +229,71 @@ __device__ __forceinline__ int wg_of_page(int p, int P, int W) {
     return w;
 }
 
-// Pages of all (sequence, kv head) units before sequence b (units are
-// ordered sequence-major, then kv head).
+// Pages of all sequences before sequence b.
 __device__ __forceinline__ int seq_page_base(const DecodeArgs &a, int b, int npg) {
-    return a.pre_seq ? a.pre_seq[b] : b * a.num_kv_heads * npg;
+    return a.pre_seq ? a.pre_seq[b] : b * npg;
 }
 
-// Stream-K decode: the pages of every (sequence, kv head) unit are laid end
-// to end and workgroup w takes pages [wg_start(w), wg_start(w+1)) — equal
-// shares, whatever the ragged lengths.  A workgroup walks the unit segments
-// of its range; a unit it covers whole is written out directly, a unit cut
-// by a range boundary leaves a partial (m, l, acc) in slot 2w (the range's
-// first unit) or 2w+1 (its last unit) for combine_kernel.
+// Per-sequence facts for sequences b0 .. b0+63, one per lane, so a sequence
+// switch costs v_readlane instead of a chain of dependent loads.
+struct SeqWindow {
+    int b0;
+    int base, ctx, sid;  // this lane's sequence: first page, length, cache slot
+};
+
+__device__ __forceinline__ void load_window(SeqWindow &win, const DecodeArgs &a, int b0, int lane) {
+    const int i = b0 + lane;
+    const bool ok = i < a.n_seqs;
+    const int npg_c = (a.ctx_len_const + 15) >> 4;
+    win.b0 = b0;
+    win.ctx = ok ? (a.ctx_lens ? a.ctx_lens[i] : a.ctx_len_const) : 0;
+    win.base = ok ? (a.pre_seq ? a.pre_seq[i] : i * npg_c) : a.total_pages;
+    win.sid = (ok && a.table) ? a.seq_ids[i] : 0;
+}
+
+// A page of the workgroup's range: sequence b (index in the step), page pg of
+// it.  Every field is wave-uniform.
+struct Cursor {
+    int b, pg, npg, ctx, base, sid;
+    bool ok;
+};
+
+__device__ __forceinline__ Cursor seq_cursor(const SeqWindow &win, int b) {
+    Cursor c;
+    const int k = b - win.b0;
+    c.b = b;
+    c.pg = 0;
+    c.ctx = __builtin_amdgcn_readlane(win.ctx, k);
+    c.base = __builtin_amdgcn_readlane(win.base, k);
+    c.sid = __builtin_amdgcn_readlane(win.sid, k);
+    c.npg = (c.ctx + 15) >> 4;
+    c.ok = true;
+    return c;
+}
+
+// Stream-K decode: the pages of every sequence are laid end to end and
+// workgroup w takes pages [wg_start(w), wg_start(w+1)) — equal shares,
+// whatever the ragged lengths.  Waves 2h and 2h+1 of the workgroup serve kv
+// head h, so the workgroup reads the Hkv head slices of the same token rows
+// together (whole 2 KB rows, whole 32 KB pages).  One pipeline walks the
+// whole range, so the first page of the next sequence is in flight while the
+// last of the current one is folded in.  At a sequence's end the two waves of
+// each head merge through LDS; a sequence the range covers whole is written
+// out directly, a sequence cut by a range boundary leaves a partial (m, l,
+// acc) per head in slot 2w (the range's first sequence) or 2w+1 (its last)
+// for combine_kernel.
 template <int G>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeArgs a) {
+    // Query rows of the range's first kQSlots sequences per head in LDS (both
+    // waves of the head read them); later ones are reloaded kQSlots at a time.
+    constexpr int kQSlots = (24 / G) > 2 ? (24 / G) : 2;
+    __shared__ uint4 q_lds[kDecodeHeadsPerWg * kQSlots * G * 32];
+    // Per-wave broadcast buffer for PV's probability pairs.
+    __shared__ uint32_t p_lds[2 * kDecodeHeadsPerWg * 32];
+    // Wave 2h+1's state for wave 2h to merge at a sequence end.
+    __shared__ float4 mrg_acc[kDecodeHeadsPerWg * G * 64];
+    __shared__ float mrg_ml[kDecodeHeadsPerWg * G * 2];
+
     const int w = blockIdx.x;
     const int W = a.n_wg;
     const int P = a.total_pages;
@@ -191,188 +302,240 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     if (p_begin >= p_end) return;  // uniform over the workgroup
     const int hkv = a.num_kv_heads;
     const int nh = a.num_heads;
-
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = threadIdx.x >> 6;
+    const int hl = wave >> 1;  // head within the workgroup
+    const int half = wave & 1;  // tokens 8*half .. 8*half+7 of each page
+    // This wave's kv head: grid.y splits the heads when more than fit one
+    // workgroup.
+    const int h = __builtin_amdgcn_readfirstlane(blockIdx.y * (blockDim.x >> 7) + hl);
     const int lane = threadIdx.x & 63;
     const int r = lane >> 4;
     const int j = lane & 15;
     const int row_bytes = hkv * kHeadDim * 2;
     const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
-    const uint32_t koff = r * row_bytes + 16 * j;
-    const uint32_t voff = 8 * lane;
+    const uint32_t koff = (kHalf * half + r) * row_bytes + 16 * j;
+    const uint32_t voff = kHalf * half * row_bytes + 8 * lane;
 
-    // Sequence holding p_begin: the last b with base(b) <= p_begin.
-    int b;
+    // Sequences holding the first and the last page of the range: the number
+    // of sequences that end at or before the page (a ballot per 64).
+    int b0, b1;
     if (a.pre_seq) {
-        int lo = 0, hi = a.n_seqs - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (a.pre_seq[mid] <= p_begin) lo = mid; else hi = mid - 1;
+        b0 = 0;
+        b1 = 0;
+        for (int c0 = 0; c0 < a.n_seqs; c0 += 64) {
+            const int i = c0 + lane;
+            const int end = i < a.n_seqs ? a.pre_seq[i + 1] : INT32_MAX;
+            const uint64_t m0 = __ballot(end <= p_begin);
+            const uint64_t m1 = __ballot(end <= p_end - 1);
+            b0 += __popcll(m0);
+            b1 += __popcll(m1);
+            if (m1 != ~0ull) break;
         }
-        b = lo;
     } else {
-        b = p_begin / (hkv * ((a.ctx_len_const + 15) >> 4));
+        const int npg_c = (a.ctx_len_const + 15) >> 4;
+        b0 = p_begin / npg_c;
+        b1 = (p_end - 1) / npg_c;
     }
+    b0 = __builtin_amdgcn_readfirstlane(b0);
+    b1 = __builtin_amdgcn_readfirstlane(b1);
+    SeqWindow win;
+    load_window(win, a, b0, lane);
 
-    __shared__ float sm_ml[kDecodeWaves][G][2];
-    __shared__ float4 sm_acc[kDecodeWaves][G][64];
-    int p = p_begin;
-    bool first_seg = true;
-    while (p < p_end) {
-        const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
-        const int npg = (ctx + 15) >> 4;
-        const int base_b = seq_page_base(a, b, npg);
-        if (npg == 0 || p >= base_b + hkv * npg) {  // empty or finished sequence
+    // Query rows of sequences b .. b+kQSlots-1 (up to b1) into this head's
+    // slots, half by each of its two waves; q_hi is the last sequence loaded.
+    // Callers pass a barrier before the rows are read.
+    uint4 *q_head = q_lds + hl * kQSlots * G * 32;
+    int q_hi = 0;
+    auto load_q = [&](int b) {
+        q_hi = b + kQSlots - 1;
+        const int n = min(kQSlots, b1 - b + 1);
+        for (int k = 0; k < n; ++k) {
+            const uint16_t *qb =
+                a.q + (static_cast<size_t>(b + k) * nh + static_cast<size_t>(h) * G) * kHeadDim;
+            const int slot = (b + k - b0) % kQSlots;
+#pragma unroll
+            for (int i = lane + 64 * half; i < G * 32; i += 128) q_head[slot * G * 32 + i] = ld16(qb + 8 * i);
+        }
+    };
+    // The current sequence's query pieces j and j+16, in registers; refilled
+    // from LDS (no memory round trip) when the walk enters a new sequence.
+    uint4 qv[G][2];
+    auto fill_q = [&](int b) {
+        const uint4 *qs = q_head + ((b - b0) % kQSlots) * G * 32;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            qv[g][0] = qs[g * 32 + j];
+            qv[g][1] = qs[g * 32 + 16 + j];
+        }
+    };
+    load_q(b0);
+    __syncthreads();
+    fill_q(b0);
+
+    const char *kpool = reinterpret_cast<const char *>(a.k_pool) + h * kHeadDim * 2;
+    const char *vpool = reinterpret_cast<const char *>(a.v_pool) + h * kHeadDim * 2;
+    auto page_id = [&](const Cursor &c) -> int {
+        return a.table ? ld_uniform(a.table + static_cast<size_t>(c.sid) * a.table_stride + c.pg) : c.pg;
+    };
+    auto page_ofs = [&](const Cursor &c, int id) -> size_t {
+        const size_t seq = a.table ? 0 : static_cast<size_t>(c.b) * a.seq_stride * 2;
+        return seq + static_cast<size_t>(id) * page_bytes;
+    };
+    auto lim_of = [](const Cursor &c) { return min(kBlockTokens, c.ctx - c.pg * kBlockTokens); };
+    // The page after c in the range (skipping empty sequences).
+    auto next = [&](Cursor c) -> Cursor {
+        if (!c.ok) return c;
+        if (c.base + c.pg + 1 >= p_end) {
+            c.ok = false;
+            return c;
+        }
+        if (c.pg + 1 < c.npg) {
+            ++c.pg;
+            return c;
+        }
+        int b = c.b;
+        do {
             ++b;
-            continue;
-        }
-        const int h = (p - base_b) / npg;
-        const int pg0 = p - base_b - h * npg;
-        const int seg_end = min(base_b + (h + 1) * npg, p_end);
-        const int pg1 = pg0 + (seg_end - p);
+            if (b - win.b0 >= 64) load_window(win, a, b, lane);
+            c = seq_cursor(win, b);
+        } while (c.npg == 0);
+        return c;
+    };
 
-        const int32_t *trow =
-            a.table ? a.table + static_cast<size_t>(a.seq_ids[b]) * a.table_stride : nullptr;
-        const size_t seq_base = a.table ? 0 : static_cast<size_t>(b) * a.seq_stride * 2;
-        const char *kpool = reinterpret_cast<const char *>(a.k_pool) + seq_base + h * kHeadDim * 2;
-        const char *vpool = reinterpret_cast<const char *>(a.v_pool) + seq_base + h * kHeadDim * 2;
-
-        uint4 qv[G][2];
-        const uint16_t *qb =
-            a.q + (static_cast<size_t>(b) * nh + static_cast<size_t>(h) * G) * kHeadDim;
+    WaveState<G> st;
+    reset(st);
+    // End of sequence c.b in this range: wave 2h+1 hands its state to wave
+    // 2h through LDS, which merges and writes the output (whole sequence) or
+    // this range's partial.  Every wave of the workgroup reaches the two
+    // barriers together: they all walk the same pages.
+    auto finish = [&](const Cursor &c, int b_next) {
+        const float qk_scale = kLog2e / 16.0f;
+        float lt[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            qv[g][0] = ld16(qb + g * kHeadDim + 8 * j);
-            qv[g][1] = ld16(qb + g * kHeadDim + 8 * (j + 16));
+        for (int g = 0; g < G; ++g) {  // the four rows hold disjoint tokens
+            lt[g] = st.l[g];
+            lt[g] += __shfl_xor(lt[g], 16);
+            lt[g] += __shfl_xor(lt[g], 32);
         }
-        WaveState<G> st;
+        if (half == 1) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            st.m[g] = -INFINITY;
-            st.l[g] = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) st.acc[g][c] = 0.0f;
-        }
-
-        // This wave's pages of the segment: first, first+4, ...  All are full
-        // except the unit's last page when the length is not a page multiple.
-        const int first = pg0 + wave;
-        const int n_pages = first < pg1 ? (pg1 - first + kDecodeWaves - 1) / kDecodeWaves : 0;
-        const int last_lim = ctx - (npg - 1) * kBlockTokens;
-        const bool owns_partial = last_lim < kBlockTokens && n_pages > 0 &&
-                                  first + (n_pages - 1) * kDecodeWaves == npg - 1;
-        const int n_full = n_pages - (owns_partial ? 1 : 0);
-        auto page_off = [&](int blk) -> size_t {
-            const int pb = trow ? __builtin_amdgcn_readfirstlane(trow[blk]) : blk;
-            return static_cast<size_t>(pb) * page_bytes;
-        };
-
-        // K of the next page is prefetched into the idle one of two register
-        // buffers; V of the current page is issued first and lands during QK.
-        KRegs KA, KB;
-        VRegs V;
-#if KVA_DEEP_PREFETCH
-        VRegs V2;
-        if (n_full > 0) {
-            load_k<true>(KA, kpool + page_off(first), koff, row_bytes, r, kBlockTokens);
-            load_v<true>(V, vpool + page_off(first), voff, row_bytes, kBlockTokens);
-        }
-        for (int i = 0; i < n_full; i += 2) {
-            if (i + 1 < n_full) {
-                const size_t o = page_off(first + (i + 1) * kDecodeWaves);
-                load_k<true>(KB, kpool + o, koff, row_bytes, r, kBlockTokens);
-                load_v<true>(V2, vpool + o, voff, row_bytes, kBlockTokens);
-            }
-            compute_page<G, true>(st, KA, V, qv, r, kBlockTokens);
-            if (i + 1 >= n_full) break;
-            if (i + 2 < n_full) {
-                const size_t o = page_off(first + (i + 2) * kDecodeWaves);
-                load_k<true>(KA, kpool + o, koff, row_bytes, r, kBlockTokens);
-                load_v<true>(V, vpool + o, voff, row_bytes, kBlockTokens);
-            }
-            compute_page<G, true>(st, KB, V2, qv, r, kBlockTokens);
-        }
-#else
-        if (n_full > 0) load_k<true>(KA, kpool + page_off(first), koff, row_bytes, r, kBlockTokens);
-        for (int i = 0; i < n_full; i += 2) {
-            load_v<true>(V, vpool + page_off(first + i * kDecodeWaves), voff, row_bytes, kBlockTokens);
-            if (i + 1 < n_full)
-                load_k<true>(KB, kpool + page_off(first + (i + 1) * kDecodeWaves), koff, row_bytes, r,
-                             kBlockTokens);
-            compute_page<G, true>(st, KA, V, qv, r, kBlockTokens);
-            if (i + 1 >= n_full) break;
-            load_v<true>(V, vpool + page_off(first + (i + 1) * kDecodeWaves), voff, row_bytes,
-                         kBlockTokens);
-            if (i + 2 < n_full)
-                load_k<true>(KA, kpool + page_off(first + (i + 2) * kDecodeWaves), koff, row_bytes, r,
-                             kBlockTokens);
-            compute_page<G, true>(st, KB, V, qv, r, kBlockTokens);
-        }
-#endif
-        if (owns_partial) {
-            const size_t o = page_off(npg - 1);
-            load_k<false>(KA, kpool + o, koff, row_bytes, r, last_lim);
-            load_v<false>(V, vpool + o, voff, row_bytes, last_lim);
-            compute_page<G, false>(st, KA, V, qv, r, last_lim);
-        }
-
-        // Merge the four waves through LDS; write the output (whole unit) or
-        // this range's partial for the unit.
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float lt = st.l[g];  // rows hold disjoint tokens: sum the four rows
-            lt += __shfl_xor(lt, 16);
-            lt += __shfl_xor(lt, 32);
-            if (lane == 0) {
-                sm_ml[wave][g][0] = st.m[g];
-                sm_ml[wave][g][1] = lt;
-            }
-            sm_acc[wave][g][lane] = make_float4(st.acc[g][0], st.acc[g][1], st.acc[g][2], st.acc[g][3]);
-        }
-        __syncthreads();
-        const bool whole = pg0 == 0 && pg1 == npg;
-        const int slot = 2 * w + (first_seg ? 0 : 1);
-        const int d = threadIdx.x;  // one output dim per thread
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float mw[kDecodeWaves];
-            float big = -INFINITY;
-#pragma unroll
-            for (int wv = 0; wv < kDecodeWaves; ++wv) {
-                mw[wv] = sm_ml[wv][g][0];
-                big = fmaxf(big, mw[wv]);
-            }
-            float lt = 0.0f, at = 0.0f;
-#pragma unroll
-            for (int wv = 0; wv < kDecodeWaves; ++wv) {
-                const float cw = (mw[wv] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw[wv] - big);
-                lt += cw * sm_ml[wv][g][1];
-                at += cw * reinterpret_cast<const float *>(&sm_acc[wv][g][0])[d];
-            }
-            if (whole) {
-                a.out[(static_cast<size_t>(b) * nh + h * G + g) * kHeadDim + d] = f2h(at / lt);
-            } else {
-                const size_t u = static_cast<size_t>(slot) * G + g;
-                a.ws_acc[u * kHeadDim + d] = at;
-                if (d == 0) {
-                    a.ws_ml[u * 2] = big;
-                    a.ws_ml[u * 2 + 1] = lt;
+            for (int g = 0; g < G; ++g) {
+                mrg_acc[(hl * G + g) * 64 + lane] = make_float4(st.acc[g][0], st.acc[g][1], st.acc[g][2], st.acc[g][3]);
+                if (lane == 0) {
+                    mrg_ml[(hl * G + g) * 2] = st.m[g];
+                    mrg_ml[(hl * G + g) * 2 + 1] = lt[g];
                 }
             }
         }
-        __syncthreads();  // LDS is reused by the next segment
-        p = seg_end;
-        first_seg = false;
+        if (b_next > q_hi) load_q(b_next);
+        __syncthreads();
+        if (half == 0) {
+            const bool whole = c.base >= p_begin && c.base + c.npg <= p_end;
+            const int slot = 2 * w + (c.b == b0 ? 0 : 1);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                // Wave 0 of the pair always saw token 0 of every page: its m is finite.
+                const float m1 = mrg_ml[(hl * G + g) * 2];
+                const float l1 = mrg_ml[(hl * G + g) * 2 + 1];
+                const float4 a1 = mrg_acc[(hl * G + g) * 64 + lane];
+                const float mm = fmaxf(st.m[g], m1);
+                const float c0 = __builtin_amdgcn_exp2f((st.m[g] - mm) * qk_scale);
+                const float c1 = __builtin_amdgcn_exp2f((m1 - mm) * qk_scale);
+                const float l = lt[g] * c0 + l1 * c1;
+                const float o0 = st.acc[g][0] * c0 + a1.x * c1;
+                const float o1 = st.acc[g][1] * c0 + a1.y * c1;
+                const float o2 = st.acc[g][2] * c0 + a1.z * c1;
+                const float o3 = st.acc[g][3] * c0 + a1.w * c1;
+                if (whole) {
+                    const float inv = 1.0f / l;
+                    uint2 o;
+                    o.x = pack_h2(o0 * inv, o1 * inv);
+                    o.y = pack_h2(o2 * inv, o3 * inv);
+                    *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(c.b) * nh + h * G + g) * kHeadDim +
+                                               4 * lane) = o;
+                } else {
+                    const size_t u = (static_cast<size_t>(slot) * hkv + h) * G + g;
+                    *reinterpret_cast<float4 *>(a.ws_acc + u * kHeadDim + 4 * lane) = make_float4(o0, o1, o2, o3);
+                    if (lane == 0) {
+                        a.ws_ml[u * 2] = mm * qk_scale;  // log2 units
+                        a.ws_ml[u * 2 + 1] = l;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        reset(st);
+    };
+
+    // Half-page buffers in a ring of kStages: while one is folded in, the
+    // next pages' halves are in flight (with three, about 128 KB per CU,
+    // what HBM's loaded latency needs; G = 8 keeps two to stay within 256
+    // VGPRs).  Every step issues the same loads (a prefetch past the range
+    // goes through an empty resource), so the compiler's load counters stay
+    // exact and waiting for one buffer never drains the others.
+    constexpr int kStages = G <= 6 ? 3 : 2;
+    HalfPage A, B, C;
+    Cursor c0 = seq_cursor(win, b0);  // window lane 0 is b0
+    c0.pg = p_begin - c0.base;
+    // cq[0] is folded in this step, cq[1..kStages-2] are in flight, and
+    // cq[kStages-1] (with id_last) is issued this step.
+    Cursor cq[kStages];
+    cq[0] = c0;
+    for (int i = 1; i < kStages; ++i) cq[i] = next(cq[i - 1]);
+    int id_last = 0;
+    {
+        int id = page_id(cq[0]);
+        load_half(A, kpool + page_ofs(cq[0], id), vpool + page_ofs(cq[0], id), lim_of(cq[0]), true, koff, voff,
+                  row_bytes);
+        if (kStages == 3) {
+            id = cq[1].ok ? page_id(cq[1]) : id;
+            load_half(B, kpool + page_ofs(cq[1], id), vpool + page_ofs(cq[1], id), lim_of(cq[1]), cq[1].ok, koff,
+                      voff, row_bytes);
+        }
+        id_last = cq[kStages - 1].ok ? page_id(cq[kStages - 1]) : id;
+    }
+    // One step: issue cq[last] into `nr`, fold cq[0] (in `cr`) in, finish the
+    // sequence when the next page belongs to another one.
+    auto step = [&](HalfPage &cr, HalfPage &nr) -> bool {
+        const Cursor cl = cq[kStages - 1];
+        const Cursor cn = next(cl);
+        const int id_n = cn.ok ? page_id(cn) : id_last;
+        load_half(nr, kpool + page_ofs(cl, id_last), vpool + page_ofs(cl, id_last), lim_of(cl), cl.ok, koff,
+                  voff, row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+        const Cursor cur = cq[0];
+        const int lim = lim_of(cur) - kHalf * half;  // valid tokens of this wave's half
+        if (lim > 0) compute_half<G>(st, cr, qv, r, j, min(lim, kHalf), p_lds + 32 * wave);
+        if (!cq[1].ok || cq[1].b != cur.b) {
+            finish(cur, cq[1].ok ? cq[1].b : 0);
+            if (cq[1].ok) fill_q(cq[1].b);
+        }
+#pragma unroll
+        for (int i = 0; i + 1 < kStages; ++i) cq[i] = cq[i + 1];
+        cq[kStages - 1] = cn;
+        id_last = id_n;
+        return cq[0].ok;
+    };
+    if constexpr (kStages == 3) {
+        while (step(A, C) && step(B, A) && step(C, B)) {
+        }
+    } else {
+        while (step(A, B) && step(B, A)) {
+        }
     }
 }
 
-// Merge the partials of one (unit, query head of its group) whose pages were
-// cut across workgroups: 64 lanes x 4 dims.  A separate launch (stream order
-// makes the partials visible), so no cross-workgroup fences are needed: an
-// agent-scope release on every decode workgroup costs an L2 writeback per
-// workgroup on multi-XCD parts.
+// Merge the partials of one (sequence, kv head, query head of the group)
+// whose pages were cut across workgroups: 64 lanes x 4 dims.  A separate
+// launch (stream order makes the partials visible), so no cross-workgroup
+// fences are needed: an agent-scope release on every decode workgroup costs
+// an L2 writeback per workgroup on multi-XCD parts.  The (m, l) pairs and acc
+// rows of up to kChunk partials are all requested before any is used, so a
+// sequence cut into at most kChunk pieces costs two memory round trips (its
+// length, then its partials).
 template <int G>
 __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
+    constexpr int kChunk = 16;
     const int u = blockIdx.x;
     const int g = blockIdx.y;
     const int hkv = a.num_kv_heads;
@@ -384,27 +547,54 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
     const int npg = (ctx + 15) >> 4;
     if (npg == 0) return;
-    const int first = seq_page_base(a, b, npg) + h * npg;
+    const int first = seq_page_base(a, b, npg);
     const int w0 = wg_of_page(first, P, W);
     const int w1 = wg_of_page(first + npg - 1, P, W);
-    if (w0 == w1) return;  // one workgroup covered the unit and wrote it
-    float big = -INFINITY;
-    for (int w = w0; w <= w1; ++w) {
+    if (w0 == w1) return;  // one workgroup covered the sequence and wrote it
+    const int n = w1 - w0 + 1;
+    // Partial i comes from workgroup w0 + i: slot 2w when the sequence began
+    // at or before that workgroup's range, else 2w+1.
+    auto row_of = [&](int i) -> size_t {
+        const int w = w0 + i;
         const int slot = 2 * w + (first <= wg_start(w, P, W) ? 0 : 1);
-        big = fmaxf(big, a.ws_ml[(static_cast<size_t>(slot) * G + g) * 2]);
-    }
-    float lt = 0.0f;
+        return (static_cast<size_t>(slot) * hkv + h) * G + g;
+    };
+    // Running merge over chunks: (big, lt, at) is the merge of the chunks so far.
+    float big = -INFINITY, lt = 0.0f;
     float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int w = w0; w <= w1; ++w) {
-        const int slot = 2 * w + (first <= wg_start(w, P, W) ? 0 : 1);
-        const size_t s = static_cast<size_t>(slot) * G + g;
-        const float c = __builtin_amdgcn_exp2f(a.ws_ml[s * 2] - big);
-        lt += c * a.ws_ml[s * 2 + 1];
-        const float4 v = reinterpret_cast<const float4 *>(a.ws_acc + s * kHeadDim)[lane];
-        at.x += c * v.x;
-        at.y += c * v.y;
-        at.z += c * v.z;
-        at.w += c * v.w;
+    for (int c0 = 0; c0 < n; c0 += kChunk) {
+        const int cnt = min(kChunk, n - c0);
+        float2 ml = make_float2(-INFINITY, 0.0f);
+        if (lane < cnt) ml = *reinterpret_cast<const float2 *>(a.ws_ml + row_of(c0 + lane) * 2);
+        float4 v[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k)
+            v[k] = k < cnt ? reinterpret_cast<const float4 *>(a.ws_acc + row_of(c0 + k) * kHeadDim)[lane]
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        float cm = ml.x;
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o));
+        cm = __shfl(cm, 0);
+        const float nb = fmaxf(big, cm);
+        const float keep = __builtin_amdgcn_exp2f(big - nb);  // 0 on the first chunk
+        const float ci = lane < cnt ? __builtin_amdgcn_exp2f(ml.x - nb) : 0.0f;
+        float ls = ci * ml.y;
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) ls += __shfl_xor(ls, o);
+        lt = lt * keep + __shfl(ls, 0);
+        at.x *= keep;
+        at.y *= keep;
+        at.z *= keep;
+        at.w *= keep;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            const float ck = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ci), k));
+            at.x += ck * v[k].x;
+            at.y += ck * v[k].y;
+            at.z += ck * v[k].z;
+            at.w += ck * v[k].w;
+        }
+        big = nb;
     }
     const float inv = 1.0f / lt;
     uint2 o;
@@ -416,7 +606,12 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
 
 template <int G>
 hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(decode_kernel<G>, dim3(a.n_wg), dim3(256), 0, s, a);
+    // Kv heads per workgroup (two waves each): all of them up to
+    // kDecodeHeadsPerWg (two waves per SIMD at 512 threads), else the largest
+    // divisor of Hkv that is at most that.
+    int hpw = a.num_kv_heads <= kDecodeHeadsPerWg ? a.num_kv_heads : kDecodeHeadsPerWg;
+    while (a.num_kv_heads % hpw) --hpw;
+    hipLaunchKernelGGL(decode_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(128 * hpw), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !a.ws_acc) return e;
     hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64), 0, s, a);

@@ -50,7 +50,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 constexpr int kStageSlots = 4;
 constexpr int kDecodeWgPerCu = 1;   // stream-K decode workgroups per CU
-constexpr int kMinPagesPerWg = 8;   // two pages per wave at least
+constexpr int kMinPagesPerWg = 2;   // a short sequence still spreads over several CUs
 constexpr int kMaxGroup = 8;        // largest GQA group the kernels take
 
 }  // namespace
@@ -76,6 +76,7 @@ struct kva_cache {
     float *d_mq_ml = nullptr;
     int32_t mq_max_wg = 0;
     int32_t max_wg = 0;  // decode workgroups the partial workspace can serve
+    size_t ws_rows = 0;  // 256-float rows in the decode partial workspace
     int32_t n_cu = 0;
 
     // pinned staging ring
@@ -97,7 +98,7 @@ struct kva_cache {
     // current step plan
     bool step_valid = false;
     int32_t st_n_seqs = 0, st_n_tok = 0, st_max_ctx = 0, st_max_new = 0, st_max_pos = 0;
-    int32_t st_total_pages = 0;  // pages of all (sequence, kv head) units
+    int32_t st_total_pages = 0;  // pages of all sequences of the step
     int32_t st_mq_units = 0;     // (sequence, 16-token tile, kv head) units
     int32_t st_mq_blocks = 0;    // 32-key blocks of all multi-query units
     size_t off_upre = 0, off_mqpre = 0;
@@ -318,10 +319,11 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
         if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess)
             return cleanup(hip_fail(e, "hipDeviceGetAttribute(CU count)"));
         c->n_cu = std::max(1, ncu);
-        // Partial slots: two per decode workgroup, each [group][256] floats;
+        // Partial slots: two per decode workgroup, each [heads][256] floats;
         // up to four workgroups per CU can be requested.
         c->max_wg = 4 * c->n_cu;
-        const size_t units = static_cast<size_t>(2) * c->max_wg * kMaxGroup;
+        c->ws_rows = static_cast<size_t>(2) * c->max_wg * c->cfg.num_heads;
+        const size_t units = c->ws_rows;
         if ((e = hipMalloc(&c->d_ws_acc, units * kva::kHeadDim * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(workspace)"));
         if ((e = hipMalloc(&c->d_ws_ml, units * 2 * sizeof(float))) != hipSuccess)
@@ -616,7 +618,7 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
         max_ctx = std::max(max_ctx, p_ctx[b]);
         max_new = std::max(max_new, n_new[b]);
         p_pre[b] = static_cast<int32_t>(pages);
-        pages += static_cast<int64_t>(c->cfg.num_kv_heads) * ((p_ctx[b] + kva::kBlockTokens - 1) / kva::kBlockTokens);
+        pages += (p_ctx[b] + kva::kBlockTokens - 1) / kva::kBlockTokens;
         all_one = all_one && n_new[b] == 1;
     }
     p_off[n_seqs] = t;
@@ -736,12 +738,13 @@ int kva_get_decode_split(const kva_cache *c, int32_t *split_tokens, int32_t *n_s
 }
 
 // Fill the stream-K fields of a decode launch over `pages` pages.
-static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_t group) {
+static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_t num_heads) {
     a.total_pages = static_cast<int32_t>(pages);
-    a.n_wg = choose_wg(c, pages);
+    // Two partial slots of num_heads rows per workgroup must fit the workspace.
+    const int64_t fit = static_cast<int64_t>(c->ws_rows / (2 * static_cast<size_t>(num_heads)));
+    a.n_wg = static_cast<int32_t>(std::max<int64_t>(1, std::min<int64_t>(choose_wg(c, pages), fit)));
     a.ws_acc = c->d_ws_acc;
     a.ws_ml = c->d_ws_ml;
-    (void)group;
     c->last_nwg = a.n_wg;
     c->last_split = static_cast<int32_t>((pages * kva::kBlockTokens + a.n_wg - 1) / a.n_wg);
 }
@@ -766,7 +769,7 @@ int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream
     a.n_seqs = c->st_n_seqs;
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
-    set_stream_k(c, a, c->st_total_pages, c->group);
+    set_stream_k(c, a, c->st_total_pages, c->cfg.num_heads);
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;
@@ -956,13 +959,13 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *k_base, const
     a.num_kv_heads = num_kv_heads;
     // Every sequence has the same length: the page prefix sums are implicit.
     const int64_t unit_pages = (kv_seq_len + kva::kBlockTokens - 1) / kva::kBlockTokens;
-    const int64_t pages = unit_pages * num_kv_heads * batch;
+    const int64_t pages = unit_pages * batch;
     if (ws) {
-        set_stream_k(ws, a, pages, g);
+        set_stream_k(ws, a, pages, num_heads);
     } else {
-        // No workspace: one workgroup per (sequence, kv head), written whole.
+        // No workspace: one workgroup per sequence, written whole.
         a.total_pages = static_cast<int32_t>(pages);
-        a.n_wg = batch * num_kv_heads;
+        a.n_wg = batch;
     }
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));

@@ -12,8 +12,8 @@ namespace kva {
 
 constexpr int kHeadDim = 256;     // the only head_dim the paged kernels take
 constexpr int kBlockTokens = 16;  // tokens per page
-constexpr int kDecodeWaves = 4;   // waves per decode workgroup
-constexpr int kSplitQuantum = 64; // decode split sizes are multiples of this
+constexpr int kDecodeHeadsPerWg = 4;  // kv heads per decode workgroup (two waves each), at most
+constexpr int kSplitQuantum = 16; // decode split sizes are whole pages
 
 // Fused QK-RMSNorm + RoPE + K/V append over all new tokens of a step.
 struct AppendArgs {
@@ -63,17 +63,17 @@ struct DecodeArgs {
     size_t seq_stride;        // contiguous cache: elements between sequences
     const int32_t *seq_ids;   // device [n_seqs] (ignored when table == null)
     const int32_t *ctx_lens;  // device [n_seqs] (null: use ctx_len_const)
-    const int32_t *pre_seq;   // device [n_seqs+1]: pages of all units of earlier
-                              // sequences (null: every sequence has ctx_len_const)
+    const int32_t *pre_seq;   // device [n_seqs+1]: pages of earlier sequences
+                              // (null: every sequence has ctx_len_const)
     int32_t ctx_len_const;
     int32_t n_seqs;
     int32_t num_heads;
     int32_t num_kv_heads;
-    int32_t total_pages;      // pages of all (sequence, kv head) units
+    int32_t total_pages;      // pages of all sequences (one page = 16 token rows)
     int32_t n_wg;             // workgroups sharing the pages (stream-K)
-    float *ws_acc;            // [2*n_wg][G][256] partial slots; null = every
-                              // unit is whole in one workgroup (no combine)
-    float *ws_ml;             // [2*n_wg][G][2]
+    float *ws_acc;            // [2*n_wg][Hkv][G][256] partial slots; null = every
+                              // sequence is whole in one workgroup (no combine)
+    float *ws_ml;             // [2*n_wg][Hkv][G][2]
     uint16_t *out;            // [n_seqs][H][256]
 };
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
