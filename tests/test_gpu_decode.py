@@ -146,7 +146,8 @@ def test_decode_special_cases(device):
 
 
 @pytest.mark.parametrize("h,hkv,L", [(4, 2, 256), (4, 4, 256), (8, 2, 512), (48, 8, 256),
-                                     (48, 8, 512), (48, 8, 1024), (24, 4, 255), (24, 4, 17)])
+                                     (48, 8, 512), (48, 8, 1024), (24, 4, 255), (24, 4, 17),
+                                     (24, 8, 300), (32, 4, 300), (8, 1, 129), (3, 1, 40)])
 def test_legacy_decode_reference_shapes(device, h, hkv, L):
     """tests/test_flash_attn_v3.py:281-312 (seed 7, x0.1 inputs); contiguous
     K/V of exactly L rows, so the last partial page must not read past them."""
@@ -161,6 +162,47 @@ def test_legacy_decode_reference_shapes(device, h, hkv, L):
     device.synchronize()
     ref = orc.attention_fp32(Q, K, V)
     assert max_err(out.numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("h,hkv", [(24, 4), (32, 4), (24, 8)])
+def test_legacy_decode_split_groups(device, h, hkv):
+    """Every GQA group width through cut sequences and the combine: a
+    workspace with 128-token splits over a contiguous cache (G = 6, 8, 3)."""
+    rng = np.random.default_rng(40 + h + hkv)
+    L = 1000
+    Q = rng.standard_normal((1, h, D), dtype=np.float32).astype(np.float16)
+    K = rng.standard_normal((L, hkv, D), dtype=np.float32).astype(np.float16)
+    V = rng.standard_normal((L, hkv, D), dtype=np.float32).astype(np.float16)
+    say(f"legacy decode split h={h} hkv={hkv}")
+    ws_cache, _, _ = build_cache([0], [[0]], extra_rows=1, fill=False)
+    ws_cache.set_decode_split(128)
+    dq, dk, dv = device.array(Q), device.array(K), device.array(V)
+    out = device.empty((1, h, D), np.float16)
+    _lib.call("kva_legacy_decode", ws_cache.handle, dq.ptr, dk.ptr, dv.ptr, out.ptr, L, h, hkv, None)
+    device.synchronize()
+    assert max_err(out.numpy(), orc.attention_fp32(Q, K, V)) <= TOL
+    ws_cache.destroy()
+
+
+def test_decode_workgroup_spanning_many_sequences(device):
+    """One workgroup walks 130 sequences of 1-2 pages: its per-lane sequence
+    window is reloaded past 64 sequences and its LDS query slots every few
+    sequences, with partial last pages throughout."""
+    rng = np.random.default_rng(77)
+    lengths = [int(x) for x in rng.integers(0, 31, 130)]
+    nblk = [(L + 1 + 15) // 16 for L in lengths]
+    perm = rng.permutation(sum(nblk))
+    ids, o = [], 0
+    for n in nblk:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say("decode one workgroup over 130 sequences")
+    cache, kr, vr = build_cache(lengths, ids, extra_rows=1, rng=rng)
+    tables = Tables(device, 64)
+    got, exp, *_ = run_decode_step(device, cache, kr, vr, lengths, rng, tables, split=16 * sum(nblk))
+    assert cache.decode_split()[1] == 1
+    assert max_err(got, exp) <= TOL
+    cache.destroy()
 
 
 def test_legacy_decode_batched_and_workspace(device):
