@@ -19,7 +19,8 @@ around each decode launch inside the timed region.  ``cpu_baseline`` is the
 numpy oracle on a bounded sample of the same workload on this host.
 
 Other workloads: --workload ctx8192 (every sequence at 8192 rows), c2
-(16 layers, B=1, 128 decode steps growing 128 -> 256 rows), copy (HBM
+(16 layers, B=1, 128 decode steps growing 128 -> 256 rows), c2graph (the
+same with the 16-layer step recorded once and replayed), copy (HBM
 stream-copy probe: the measured bandwidth ceiling).
 """
 from __future__ import annotations
@@ -37,7 +38,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from mi50grad_amd import _lib  # noqa: E402
-from mi50grad_amd.device import Event, GPUDevice  # noqa: E402
+from mi50grad_amd.device import Event, GPUDevice, Stream  # noqa: E402
 from mi50grad_amd.kv_cache import PagedKVCache  # noqa: E402
 from mi50grad_amd.rope import rope_tables  # noqa: E402
 from mi50grad_amd import workloads as wl  # noqa: E402
@@ -143,33 +144,57 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
     }
 
 
-def c2_workload(dev, steps_unused, warmup):
-    """Config 2: B=1, 16 layers, 128 decode steps from a 128-row cache."""
+def c2_workload(dev, steps_unused, warmup, graph=False, split=0):
+    """Config 2: B=1, 16 layers, 128 decode steps from a 128-row cache.  With
+    graph=True the 16 layers' append + decode are recorded once (kva_graph_*)
+    and replayed after each step's plan upload."""
     B, start, n_steps = 1, 128, 128
     cache = PagedKVCache(n_layers=LAYERS, max_seqs=1, max_blocks=16, max_blocks_per_seq=16,
                          max_step_tokens=16)
     cache.reserve(0, 256)
     cache.sync_tables()
+    cache.set_decode_split(split)
     fill_pools(dev, cache, 16)
     cos, sin = rope_tables(256)
     d_cos, d_sin = dev.array(cos), dev.array(sin)
     inputs = make_inputs(dev, B)
+    stream = Stream() if graph else None
+    sh = stream.handle if graph else None
+    recorded = []
+
+    def layers():
+        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 256, stream=sh)
+            cache.decode(layer, q, out, stream=sh)
 
     def run():
         cache.set_len(0, start)
         for _ in range(n_steps):
-            cache.begin_step([0], [1])
-            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
-                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 256)
-                cache.decode(layer, q, out)
+            cache.begin_step([0], [1], stream=sh)
+            if not graph:
+                layers()
+                continue
+            if not recorded:
+                g = cache.record_step(sh)
+                layers()
+                recorded.append(g.end())
+            recorded[0].launch()
 
     for _ in range(max(1, warmup)):
         run()
+    if stream:
+        stream.synchronize()
     dev.synchronize()
     t0 = time.perf_counter()
     run()
+    if stream:
+        stream.synchronize()
     dev.synchronize()
     wall = time.perf_counter() - t0
+    for g in recorded:
+        g.destroy()
+    if stream:
+        stream.destroy()
     cache.destroy()
     kv = LAYERS * ROW_BYTES * sum(range(start + 1, start + n_steps + 1))
     return {"wall_s": wall, "steps": n_steps, "kv_bytes": kv}
@@ -358,7 +383,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "c4", "c5", "copy"])
+    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "c2graph", "c4", "c5", "copy"])
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -374,14 +399,17 @@ def main() -> int:
                           "n_gpus": 1, "avg_us": r["avg_us"], "bytes_per_launch": r["bytes_per_launch"],
                           "higher_is_better": True}))
         return 0
-    if args.workload == "c2":
-        r = c2_workload(dev, args.steps, args.warmup)
+    if args.workload in ("c2", "c2graph"):
+        graph = args.workload == "c2graph"
+        r = c2_workload(dev, args.steps, args.warmup, graph=graph, split=args.split)
         ms = r["wall_s"] * 1e3 / r["steps"]
         print(json.dumps({"metric": "config-2 decode step time (16 layers, B=1, 128->256 rows)",
                           "value": ms * 1e3, "unit": "us/step", "n_gpus": 1, "steps": r["steps"],
                           "ms_per_step": ms, "higher_is_better": False,
                           "kv_gbs": r["kv_bytes"] / r["wall_s"] / 1e9, "dtype": "f16",
-                          "data": "synthetic", "config": {"workload": "C2"}}))
+                          "data": "synthetic",
+                          "config": {"workload": "C2", "dispatch": "recorded step replay" if graph
+                                     else "per-layer calls"}}))
         return 0
 
     if args.workload == "c4":

@@ -33,6 +33,7 @@ extern "C" {
 typedef void *kva_stream_t;
 typedef void *kva_event_t;
 typedef struct kva_cache kva_cache;
+typedef struct kva_graph kva_graph;
 
 enum {
     KVA_OK = 0,
@@ -191,6 +192,29 @@ int kva_rollback(kva_cache *cache, int32_t n_seqs, const int32_t *seq_ids,
 int kva_set_decode_split(kva_cache *cache, int32_t split_tokens);
 int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,
                          int32_t *n_splits);
+
+/* ---- recorded steps (hipGraph replay) ------------------------------------ */
+/* Replaces the per-step kernel-node patching of the reference's graph
+ * dispatch (c_graph_dispatch.c:392-414 update_mutable_params, which rewrote
+ * cos/sin pointers, the K slot pointer and seq_len in every node) and the
+ * C dispatch loop's patched arguments (c_dispatch.c:426-456).  Here every
+ * per-step value already lives in the device step plan that kva_step_begin
+ * uploads, so a recorded step needs no patching: record one step's
+ * kva_append_qknorm_rope and kva_decode calls (any layers, in order) between
+ * capture_begin and capture_end on one created stream, then for each later
+ * step call kva_step_begin and kva_graph_launch.  A replay is valid while
+ * the step has the recorded shape (same number of sequences, one new token
+ * each) and its RoPE positions stay within the tables the recording used;
+ * lengths may grow past page boundaries (the decode launch derives its
+ * stream-K shape from the plan on the device).  While recording, calls that
+ * cannot be recorded (kva_step_begin, kva_sync_tables, kva_prefill,
+ * kva_tree_verify, kva_rollback, kva_destroy, calls on another stream) return
+ * KVA_ERR_STATE; a failed call makes capture_end discard the recording.
+ * Destroy a graph before its cache.                                        */
+int kva_graph_capture_begin(kva_cache *cache, kva_stream_t stream);
+int kva_graph_capture_end(kva_cache *cache, kva_stream_t stream, kva_graph **out);
+int kva_graph_launch(kva_graph *graph, kva_stream_t stream);
+int kva_graph_destroy(kva_graph *graph);
 
 /* ---- reference-kernel-compatible entry points (contiguous caches) ------- */
 /* qknorm_rope_fused / qknorm_rope_cachew_fused on a contiguous

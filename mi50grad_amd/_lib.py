@@ -73,6 +73,10 @@ SIGNATURES = {
     "kva_rollback": [_P, _I, _PI, _PI, _PI, _PI, _P],
     "kva_set_decode_split": [_P, _I],
     "kva_get_decode_split": [_P, _PI, _PI],
+    "kva_graph_capture_begin": [_P, _P],
+    "kva_graph_capture_end": [_P, _P, POINTER(c_void_p)],
+    "kva_graph_launch": [_P, _P],
+    "kva_graph_destroy": [_P],
     "kva_legacy_qknorm_rope": [_P, _P, _P, _P, _P, _I, _I, _I, c_float, _P],
     "kva_legacy_decode": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
     "kva_legacy_decode_batched": [_P, _P, _P, _P, _P, _I, _I, c_int64, _I, _I, _P],

@@ -229,6 +229,22 @@ __device__ __forceinline__ int wg_of_page(int p, int P, int W) {
     return w;
 }
 
+// The stream-K shape of a launch: P pages over W workgroups.  Fixed by the
+// host for an ordinary call; for a launch recorded into a graph it is derived
+// here from the step plan (the same rule the host applies), so a replay after
+// the lengths grew still shares the right page count.
+__device__ __forceinline__ void stream_k_shape(const DecodeArgs &a, int &P, int &W) {
+    if (!a.dyn) {
+        P = a.total_pages;
+        W = a.n_wg;
+        return;
+    }
+    P = ld_uniform(a.pre_seq + a.n_seqs);
+    int w = a.split_tokens > 0 ? (P * kBlockTokens + a.split_tokens - 1) / a.split_tokens : a.n_wg;
+    w = min(w, (P + a.min_pages - 1) / a.min_pages);
+    W = max(1, min(w, a.n_wg));
+}
+
 // Pages of all sequences before sequence b.
 __device__ __forceinline__ int seq_page_base(const DecodeArgs &a, int b, int npg) {
     return a.pre_seq ? a.pre_seq[b] : b * npg;
@@ -247,7 +263,7 @@ __device__ __forceinline__ void load_window(SeqWindow &win, const DecodeArgs &a,
     const int npg_c = (a.ctx_len_const + 15) >> 4;
     win.b0 = b0;
     win.ctx = ok ? (a.ctx_lens ? a.ctx_lens[i] : a.ctx_len_const) : 0;
-    win.base = ok ? (a.pre_seq ? a.pre_seq[i] : i * npg_c) : a.total_pages;
+    win.base = ok ? (a.pre_seq ? a.pre_seq[i] : i * npg_c) : INT32_MAX;  // lanes past n_seqs: unused
     win.sid = (ok && a.table) ? a.seq_ids[i] : 0;
 }
 
@@ -295,8 +311,9 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
     __shared__ float mrg_ml[kDecodeHeadsPerWg * G * 2];
 
     const int w = blockIdx.x;
-    const int W = a.n_wg;
-    const int P = a.total_pages;
+    int P, W;
+    stream_k_shape(a, P, W);
+    if (w >= W) return;  // a recorded launch's grid is the cap
     const int p_begin = wg_start(w, P, W);
     const int p_end = wg_start(w + 1, P, W);
     if (p_begin >= p_end) return;  // uniform over the workgroup
@@ -542,8 +559,8 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
     const int b = u / hkv;
     const int h = u - b * hkv;
     const int lane = threadIdx.x;
-    const int W = a.n_wg;
-    const int P = a.total_pages;
+    int P, W;
+    stream_k_shape(a, P, W);
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
     const int npg = (ctx + 15) >> 4;
     if (npg == 0) return;

@@ -50,7 +50,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 constexpr int kStageSlots = 4;
 constexpr int kDecodeWgPerCu = 1;   // stream-K decode workgroups per CU
-constexpr int kMinPagesPerWg = 2;   // a short sequence still spreads over several CUs
+constexpr int kMinPagesPerWg = 1;   // a short sequence still spreads over several CUs
 constexpr int kMaxGroup = 8;        // largest GQA group the kernels take
 
 }  // namespace
@@ -108,6 +108,23 @@ struct kva_cache {
 
     int32_t split_user = 0;  // decode tokens per workgroup (0 = automatic)
     int32_t last_split = 0, last_nwg = 0;
+
+    // Graph recording (kva_graph_capture_begin .. _end) on `cap_stream`.
+    bool capturing = false;
+    bool capture_failed = false;
+    hipStream_t cap_stream = nullptr;
+    int32_t cap_table_rows = 0;  // fewest RoPE table rows any recorded append was given
+};
+
+// A recorded step: the launches of one step's per-layer calls, replayable for
+// any later step of the same shape (the per-step values live in the device
+// step plan, whose layout depends only on that shape).
+struct kva_graph {
+    kva_cache *cache = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int32_t n_seqs = 0, n_tok = 0, table_rows = 0;
+    bool all_one = false, has_bits = false;
+    size_t offs[11] = {};
 };
 
 namespace {
@@ -257,6 +274,28 @@ int32_t choose_wg(const kva_cache *c, int64_t pages) {
     return static_cast<int32_t>(std::max<int64_t>(1, w));
 }
 
+// While a graph is being recorded, a call on another stream would run now
+// instead of being recorded, and a call that fails leaves a hole in the
+// recording: both are refused or remembered, and kva_graph_capture_end
+// reports them.
+int capture_check(kva_cache *c, kva_stream_t stream) {
+    if (c && c->capturing && static_cast<hipStream_t>(stream) != c->cap_stream)
+        return fail(KVA_ERR_STATE, "call on another stream while a graph is being recorded");
+    return KVA_OK;
+}
+
+int capture_note(kva_cache *c, int rc) {
+    if (rc != KVA_OK && c && c->capturing) c->capture_failed = true;
+    return rc;
+}
+
+// A call that cannot be recorded: its launch shape or its host work depends
+// on the step (or it is the step change itself).
+int refuse_while_capturing(const kva_cache *c, const char *what) {
+    if (c && c->capturing) return fail(KVA_ERR_STATE, "%s cannot run while a graph is being recorded", what);
+    return KVA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -350,6 +389,7 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
 
 int kva_destroy(kva_cache *c) {
     if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (int rc = refuse_while_capturing(c, "kva_destroy")) return rc;
     if (!c->host_only) {
         (void)hipDeviceSynchronize();
         for (int i = 0; i < kStageSlots; ++i) {
@@ -509,12 +549,14 @@ int kva_row_ptr(const kva_cache *c, int32_t layer, int32_t seq, int32_t slot, vo
 
 int kva_sync_tables(kva_cache *c, kva_stream_t stream) {
     if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (int rc = refuse_while_capturing(c, "kva_sync_tables")) return rc;
     return flush_patches(c, static_cast<hipStream_t>(stream));
 }
 
 int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int32_t *n_new,
                    const int32_t *rope_pos, const uint64_t *tree_bits, kva_stream_t stream) {
     if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (int rc = refuse_while_capturing(c, "kva_step_begin")) return rc;
     c->step_valid = false;
     if (n_seqs <= 0 || n_seqs > c->cfg.max_seqs)
         return fail(KVA_ERR_INVALID_ARG, "n_seqs %d outside [1, %d]", n_seqs, c->cfg.max_seqs);
@@ -679,9 +721,9 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     return KVA_OK;
 }
 
-int kva_append_qknorm_rope(kva_cache *c, int32_t layer, void *q, void *k, const void *v,
-                           const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
-                           const void *sin_tab, int32_t table_rows, kva_stream_t stream) {
+static int append_impl(kva_cache *c, int32_t layer, void *q, void *k, const void *v, const void *q_norm_w,
+                       const void *k_norm_w, const void *cos_tab, const void *sin_tab, int32_t table_rows,
+                       kva_stream_t stream) {
     int rc = require_device(c);
     if (rc) return rc;
     if ((rc = check_layer(c, layer))) return rc;
@@ -749,7 +791,7 @@ static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_
     c->last_split = static_cast<int32_t>((pages * kva::kBlockTokens + a.n_wg - 1) / a.n_wg);
 }
 
-int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
+static int decode_impl(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
     int rc = require_device(c);
     if (rc) return rc;
     if ((rc = check_layer(c, layer))) return rc;
@@ -770,13 +812,41 @@ int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
     set_stream_k(c, a, c->st_total_pages, c->cfg.num_heads);
+    if (c->capturing) {
+        // Recorded launch: the device derives the page count and workgroup
+        // count from the step plan at replay; the grid is the cap.
+        const int64_t fit = static_cast<int64_t>(c->ws_rows / (2 * static_cast<size_t>(c->cfg.num_heads)));
+        const int64_t cap = c->split_user > 0 ? c->max_wg : static_cast<int64_t>(c->n_cu) * kDecodeWgPerCu;
+        a.n_wg = static_cast<int32_t>(std::max<int64_t>(1, std::min(cap, fit)));
+        a.dyn = 1;
+        a.split_tokens = c->split_user;
+        a.min_pages = kMinPagesPerWg;
+    }
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;
 }
 
+int kva_append_qknorm_rope(kva_cache *c, int32_t layer, void *q, void *k, const void *v,
+                           const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                           const void *sin_tab, int32_t table_rows, kva_stream_t stream) {
+    int rc = capture_check(c, stream);
+    if (rc) return capture_note(c, rc);
+    rc = append_impl(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, stream);
+    if (rc == KVA_OK && c->capturing && c->st_n_tok > 0)
+        c->cap_table_rows = c->cap_table_rows ? std::min(c->cap_table_rows, table_rows) : table_rows;
+    return capture_note(c, rc);
+}
+
+int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
+    int rc = capture_check(c, stream);
+    if (rc) return capture_note(c, rc);
+    return capture_note(c, decode_impl(c, layer, q, out, stream));
+}
+
 static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream,
                        bool tree) {
+    if (int rc = refuse_while_capturing(c, tree ? "kva_tree_verify" : "kva_prefill")) return rc;
     int rc = require_device(c);
     if (rc) return rc;
     if ((rc = check_layer(c, layer))) return rc;
@@ -828,6 +898,7 @@ int kva_tree_verify(kva_cache *c, int32_t layer, const void *q, void *out, kva_s
 int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int32_t *base_len,
                  const int32_t *keep_off, const int32_t *keep_rows, kva_stream_t stream) {
     if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (int rc = refuse_while_capturing(c, "kva_rollback")) return rc;
     if (n_seqs < 0 || n_seqs > c->cfg.max_seqs) return fail(KVA_ERR_INVALID_ARG, "bad n_seqs %d", n_seqs);
     if (n_seqs == 0) return KVA_OK;
     if (!seq_ids || !base_len || !keep_off) return fail(KVA_ERR_INVALID_ARG, "NULL index array");
@@ -896,6 +967,80 @@ int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int
     a.n_groups = n_groups;
     a.num_kv_heads = c->cfg.num_kv_heads;
     KVA_HIP(kva::launch_rollback(a, st));
+    return KVA_OK;
+}
+
+int kva_graph_capture_begin(kva_cache *c, kva_stream_t stream) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if (c->capturing) return fail(KVA_ERR_STATE, "a graph is already being recorded");
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    if (!stream) return fail(KVA_ERR_INVALID_ARG, "recording needs a created stream, not the legacy default stream");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    KVA_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    c->capture_failed = false;
+    c->cap_stream = s;
+    c->cap_table_rows = 0;
+    return KVA_OK;
+}
+
+int kva_graph_capture_end(kva_cache *c, kva_stream_t stream, kva_graph **out) {
+    if (!c || !out) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    *out = nullptr;
+    if (!c->capturing) return fail(KVA_ERR_STATE, "no graph is being recorded");
+    if (static_cast<hipStream_t>(stream) != c->cap_stream)
+        return fail(KVA_ERR_INVALID_ARG, "recording was begun on another stream");
+    c->capturing = false;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(c->cap_stream, &graph);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    if (c->capture_failed) {
+        (void)hipGraphDestroy(graph);
+        return fail(KVA_ERR_STATE, "a call failed while the graph was being recorded; nothing was kept");
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    auto *g = new kva_graph;
+    g->cache = c;
+    g->exec = exec;
+    g->n_seqs = c->st_n_seqs;
+    g->n_tok = c->st_n_tok;
+    g->table_rows = c->cap_table_rows;
+    g->all_one = c->st_all_one;
+    g->has_bits = c->st_has_bits;
+    const size_t offs[11] = {c->off_seq,  c->off_ctx,  c->off_start, c->off_tokoff, c->off_tseq, c->off_tslot,
+                             c->off_tpos, c->off_bits, c->off_pre,   c->off_upre,   c->off_mqpre};
+    std::memcpy(g->offs, offs, sizeof(offs));
+    *out = g;
+    return KVA_OK;
+}
+
+int kva_graph_launch(kva_graph *g, kva_stream_t stream) {
+    if (!g || !g->cache) return fail(KVA_ERR_INVALID_ARG, "graph is NULL");
+    kva_cache *c = g->cache;
+    if (c->capturing) return fail(KVA_ERR_STATE, "a graph is being recorded");
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    const size_t offs[11] = {c->off_seq,  c->off_ctx,  c->off_start, c->off_tokoff, c->off_tseq, c->off_tslot,
+                             c->off_tpos, c->off_bits, c->off_pre,   c->off_upre,   c->off_mqpre};
+    if (c->st_n_seqs != g->n_seqs || c->st_n_tok != g->n_tok || c->st_all_one != g->all_one ||
+        c->st_has_bits != g->has_bits || std::memcmp(offs, g->offs, sizeof(offs)) != 0)
+        return fail(KVA_ERR_STATE, "the current step (%d sequences, %d tokens) is not the recorded shape (%d, %d)",
+                    c->st_n_seqs, c->st_n_tok, g->n_seqs, g->n_tok);
+    if (g->table_rows > 0 && c->st_max_pos >= g->table_rows)
+        return fail(KVA_ERR_INVALID_ARG, "RoPE position %d beyond the %d table rows the graph was recorded with",
+                    c->st_max_pos, g->table_rows);
+    KVA_HIP(hipGraphLaunch(g->exec, static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
+int kva_graph_destroy(kva_graph *g) {
+    if (!g) return fail(KVA_ERR_INVALID_ARG, "graph is NULL");
+    hipError_t e = g->exec ? hipGraphExecDestroy(g->exec) : hipSuccess;
+    delete g;
+    if (e != hipSuccess) return hip_fail(e, "hipGraphExecDestroy");
     return KVA_OK;
 }
 

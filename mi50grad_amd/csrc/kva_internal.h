@@ -71,6 +71,12 @@ struct DecodeArgs {
     int32_t num_kv_heads;
     int32_t total_pages;      // pages of all sequences (one page = 16 token rows)
     int32_t n_wg;             // workgroups sharing the pages (stream-K)
+    // dyn = 1 (a launch recorded into a replayable graph): total_pages is
+    // read from pre_seq[n_seqs] on the device and the workgroup count derived
+    // there from split_tokens / min_pages, with n_wg as the cap (the grid).
+    int32_t dyn;
+    int32_t split_tokens;     // 0 = one workgroup per CU up to the cap
+    int32_t min_pages;
     float *ws_acc;            // [2*n_wg][Hkv][G][256] partial slots; null = every
                               // sequence is whole in one workgroup (no combine)
     float *ws_ml;             // [2*n_wg][Hkv][G][2]

@@ -165,6 +165,12 @@ class PagedKVCache:
         _lib.call("kva_rollback", self.handle, len(seq_ids), _lib.int_array(seq_ids),
                   _lib.int_array(base_len), _lib.int_array(off), _lib.int_array(flat), stream)
 
+    def record_step(self, stream) -> "StepGraph":
+        """Start recording this step's append/decode calls on `stream` (a
+        created Stream's handle); end with StepGraph.end()."""
+        _lib.call("kva_graph_capture_begin", self.handle, stream)
+        return StepGraph(self, stream)
+
     def set_decode_split(self, split_tokens: int) -> None:
         _lib.call("kva_set_decode_split", self.handle, split_tokens)
 
@@ -260,3 +266,27 @@ class KVCache:
 
     def cleanup(self):
         self.paged.destroy()
+
+
+class StepGraph:
+    """A recorded step (kva_graph_*): replay it after each begin_step of the
+    same shape instead of issuing the per-layer calls again."""
+
+    def __init__(self, cache: PagedKVCache, stream):
+        self.cache = cache
+        self.stream = stream
+        self.handle = None
+
+    def end(self) -> "StepGraph":
+        h = ctypes.c_void_p()
+        _lib.call("kva_graph_capture_end", self.cache.handle, self.stream, ctypes.byref(h))
+        self.handle = h.value
+        return self
+
+    def launch(self, stream=None) -> None:
+        _lib.call("kva_graph_launch", self.handle, self.stream if stream is None else stream)
+
+    def destroy(self) -> None:
+        if self.handle:
+            _lib.call("kva_graph_destroy", self.handle)
+            self.handle = None

@@ -1,0 +1,113 @@
+"""GPU: recorded steps (kva_graph_*) replay bit-identically to eager calls.
+
+Two caches built from the same seed: one runs every step's per-layer
+append + decode eagerly, the other records one step into a graph and replays
+it for 20 more steps, with fresh inputs uploaded between replays (the eager
+work and synchronizations between them), lengths crossing page boundaries
+(so the decode's stream-K shape changes under the recording) and a decode
+split set.  Every replayed step's outputs and, at the end, every pool byte
+must equal the eager twin's.  Also: what recording refuses, and a replay
+whose step has another shape.
+"""
+import numpy as np
+import pytest
+
+from mi50grad_amd._lib import KvaError
+from mi50grad_amd.device import Stream
+
+from gpu_helpers import HKV, H, D, Tables, build_cache, say
+
+pytestmark = pytest.mark.gpu
+LAYERS = 3
+
+
+def _twin(lengths, split, seed):
+    ids, o = [], 0
+    for L in lengths:
+        n = (L + 40 + 15) // 16
+        ids.append(list(range(o, o + n))[::-1])  # reversed: pages out of order
+        o += n
+    caches = []
+    for _ in range(2):
+        c, _, _ = build_cache(lengths, ids, extra_rows=40, n_layers=LAYERS, rng=np.random.default_rng(seed))
+        c.set_decode_split(split)
+        caches.append(c)
+    return caches
+
+
+@pytest.mark.parametrize("lengths,split", [([14, 30], 0), ([200, 5, 77], 32)])
+def test_graph_replay_matches_eager(device, lengths, split):
+    say(f"graph replay lengths={lengths} split={split}")
+    rng = np.random.default_rng(5)
+    eager, graphed = _twin(lengths, split, seed=11)
+    B = len(lengths)
+    tables = Tables(device, 512)
+    stream = Stream()
+    qw = [device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)) for _ in range(LAYERS)]
+    kw = [device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)) for _ in range(LAYERS)]
+
+    def fresh(shape):
+        return rng.standard_normal(shape, dtype=np.float32).astype(np.float16)
+
+    # One set of device inputs and outputs per cache and layer; the graph
+    # reads and writes the same buffers at every replay.
+    bufs = []
+    for _ in range(2):
+        bufs.append([dict(q=device.empty((B, H, D), np.float16), k=device.empty((B, HKV, D), np.float16),
+                          v=device.empty((B, HKV, D), np.float16), out=device.empty((B, H, D), np.float16))
+                     for _ in range(LAYERS)])
+
+    def upload(step_inputs):
+        for which in range(2):
+            for layer in range(LAYERS):
+                for name in ("q", "k", "v"):
+                    a = step_inputs[layer][name]
+                    device.upload(bufs[which][layer][name].ptr, a.tobytes())
+
+    def calls(cache, which, stream_h):
+        for layer in range(LAYERS):
+            b = bufs[which][layer]
+            cache.append(layer, b["q"], b["k"], b["v"], qw[layer], kw[layer], tables.d_cos, tables.d_sin,
+                         tables.rows, stream=stream_h)
+            cache.decode(layer, b["q"], b["out"], stream=stream_h)
+
+    graph = None
+    for step in range(21):
+        inputs = [dict(q=fresh((B, H, D)), k=fresh((B, HKV, D)), v=fresh((B, HKV, D))) for _ in range(LAYERS)]
+        upload(inputs)
+        device.synchronize()
+        eager.begin_step(list(range(B)), [1] * B)
+        calls(eager, 0, None)
+        graphed.begin_step(list(range(B)), [1] * B, stream=stream.handle)
+        if graph is None:
+            graph = graphed.record_step(stream.handle)
+            with pytest.raises(KvaError):  # the step cannot change while recording
+                graphed.begin_step(list(range(B)), [1] * B, stream=stream.handle)
+            with pytest.raises(KvaError):  # nor can a multi-query launch be recorded
+                graphed.prefill(0, bufs[1][0]["q"], bufs[1][0]["out"], stream=stream.handle)
+            calls(graphed, 1, stream.handle)
+            graph.end()
+        graph.launch()
+        stream.synchronize()
+        device.synchronize()
+        for layer in range(LAYERS):
+            got = bufs[1][layer]["out"].numpy().view(np.uint16)
+            exp = bufs[0][layer]["out"].numpy().view(np.uint16)
+            assert np.array_equal(got, exp), (step, layer)
+            assert np.array_equal(bufs[1][layer]["q"].numpy().view(np.uint16),
+                                  bufs[0][layer]["q"].numpy().view(np.uint16)), (step, layer)
+    for layer in range(LAYERS):
+        ke, ve = eager.download_pools(layer)
+        kg, vg = graphed.download_pools(layer)
+        assert np.array_equal(ke.view(np.uint16), kg.view(np.uint16))
+        assert np.array_equal(ve.view(np.uint16), vg.view(np.uint16))
+    assert [graphed.seq_len(b) for b in range(B)] == [L + 21 for L in lengths]
+    # A step of another shape is refused.
+    graphed.begin_step([0], [1], stream=stream.handle)
+    with pytest.raises(KvaError):
+        graph.launch()
+    graph.destroy()
+    stream.synchronize()
+    stream.destroy()
+    eager.destroy()
+    graphed.destroy()

@@ -169,3 +169,28 @@ def test_decode_split_setting():
     c.set_decode_split(128)
     with pytest.raises(KvaError):
         c.set_decode_split(100)
+
+
+def test_graph_recording_validation():
+    """kva_graph_*: a host-only cache cannot record; NULL graphs and an end
+    without a begin are refused before anything touches a device."""
+    import ctypes
+
+    from mi50grad_amd import _lib
+
+    c = make()
+    c.reserve(0, 3)
+    c.begin_step([0], [1])
+    with pytest.raises(KvaError) as e:
+        _lib.call("kva_graph_capture_begin", c.handle, None)
+    assert code(e) == -3
+    h = ctypes.c_void_p()
+    with pytest.raises(KvaError) as e:
+        _lib.call("kva_graph_capture_end", c.handle, None, ctypes.byref(h))
+    assert code(e) == -8
+    with pytest.raises(KvaError) as e:
+        _lib.call("kva_graph_launch", None, None)
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        _lib.call("kva_graph_destroy", None)
+    assert code(e) == -1
