@@ -162,6 +162,15 @@ int kva_append_qknorm_rope(kva_cache *cache, int32_t layer, void *q, void *k,
  * ragged per-sequence lengths.  q, out: [n_seqs, num_heads, 256] fp16.     */
 int kva_decode(kva_cache *cache, int32_t layer, const void *q, void *out,
                kva_stream_t stream);
+/* kva_decode with the attention output gate fused into its epilogue:
+ * out = fp16(fp16(attn) * 1/(1+exp(-gate))) elementwise, which is what
+ * _launch_sigmoid_mul (sigmoid_mul.hip:10-22) does to the decode output at
+ * engine.py:2055-2056, without the extra launch and round trip.  gate:
+ * fp16, sequence b's row of num_heads*256 values at gate + b*gate_stride
+ * (e.g. gate_stride = 2*num_heads*256 when it is the Q_gate half of a fused
+ * [Q | Q_gate] projection output, engine.py:1069-1071); 8-byte aligned.     */
+int kva_decode_gated(kva_cache *cache, int32_t layer, const void *q, const void *gate,
+                     int64_t gate_stride, void *out, kva_stream_t stream);
 /* Causal attention of each sequence's new rows over cache + new rows: new
  * token i (slot s) sees slots [0, s].  Replaces the prefill attention of
  * _prefill_full_attention (engine.py:3043-3139; flash_attn_256_fp16,
@@ -234,6 +243,13 @@ int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row,
 int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base,
                       const void *v_base, void *out, int32_t kv_seq_len,
                       int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream);
+/* kva_legacy_decode followed by the output gate (as kva_decode_gated) in
+ * one call: the engine's decode + _launch_sigmoid_mul pair
+ * (engine.py:2047-2056).  gate: [num_heads, 256] fp16, 8-byte aligned.     */
+int kva_legacy_decode_gated(kva_cache *ws, const void *q, const void *gate,
+                            const void *k_base, const void *v_base, void *out,
+                            int32_t kv_seq_len, int32_t num_heads, int32_t num_kv_heads,
+                            kva_stream_t stream);
 /* The intended semantics of _launch_decode_attn_256_batched
  * (engine.py:2806-2857; its kernel ignores the batch index, survey fact F9):
  * sequence b's contiguous cache starts at k_base/v_base + b*batch_stride

@@ -68,6 +68,7 @@ SIGNATURES = {
     "kva_step_begin": [_P, _I, _PI, _PI, _PI, POINTER(c_uint64), _P],
     "kva_append_qknorm_rope": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "kva_decode": [_P, _I, _P, _P, _P],
+    "kva_decode_gated": [_P, _I, _P, _P, c_int64, _P, _P],
     "kva_prefill": [_P, _I, _P, _P, _P],
     "kva_tree_verify": [_P, _I, _P, _P, _P],
     "kva_rollback": [_P, _I, _PI, _PI, _PI, _PI, _P],
@@ -79,6 +80,7 @@ SIGNATURES = {
     "kva_graph_destroy": [_P],
     "kva_legacy_qknorm_rope": [_P, _P, _P, _P, _P, _I, _I, _I, c_float, _P],
     "kva_legacy_decode": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "kva_legacy_decode_gated": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "kva_legacy_decode_batched": [_P, _P, _P, _P, _P, _I, _I, c_int64, _I, _I, _P],
     "kva_hbm_copy": [_P, _P, c_size_t, _P],
     "kva_dev_count": [_PI],

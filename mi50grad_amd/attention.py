@@ -74,6 +74,12 @@ class FullAttentionLaunchers:
         _lib.call("kva_legacy_decode", self._workspace(), q, k_cache, v_cache, out, seq_len,
                   self.local_num_attention_heads, self.local_num_kv_heads, self.stream)
 
+    def _launch_decode_attn_256_gated(self, out, q, gate, k_cache, v_cache, seq_len):
+        """The engine's decode + _launch_sigmoid_mul pair (engine.py:2047-2056)
+        in one launch: out = fp16(fp16(attn) * sigmoid(gate))."""
+        _lib.call("kva_legacy_decode_gated", self._workspace(), q, gate, k_cache, v_cache, out, seq_len,
+                  self.local_num_attention_heads, self.local_num_kv_heads, self.stream)
+
     def _launch_decode_attn_256_batched(self, out_batch, q_batch, k_cache_base, v_cache_base,
                                         seq_len, batch_size, batch_stride: int | None = None):
         if batch_stride is None:

@@ -217,6 +217,31 @@ __device__ __forceinline__ void compute_half(WaveState<G> &st, const HalfPage &p
     }
 }
 
+// Four output dims o0..o3 as fp16, through the optional output gate: the
+// attention value is rounded to fp16 first and then multiplied by
+// 1/(1+exp(-g)) in float32 (sigmoid_mul.hip:10-22 applied to the decode
+// output, engine.py:2055-2056), so the fused result equals the reference's
+// two launches.  g4: the four gate values (8-byte aligned) or null.
+__device__ __forceinline__ uint2 out_fp16x4(float o0, float o1, float o2, float o3, const uint16_t *g4) {
+    uint2 o;
+    o.x = pack_h2(o0, o1);
+    o.y = pack_h2(o2, o3);
+    if (!g4) return o;
+    const uint2 gw = *reinterpret_cast<const uint2 *>(g4);
+    const float g[4] = {lo_f(gw.x), hi_f(gw.x), lo_f(gw.y), hi_f(gw.y)};
+    const float a[4] = {lo_f(o.x), hi_f(o.x), lo_f(o.y), hi_f(o.y)};
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = a[i] * (1.0f / (1.0f + expf(-g[i])));
+    o.x = pack_h2(r[0], r[1]);
+    o.y = pack_h2(r[2], r[3]);
+    return o;
+}
+
+__device__ __forceinline__ const uint16_t *gate_of(const DecodeArgs &a, int b, int hq, int lane) {
+    return a.gate ? a.gate + static_cast<int64_t>(b) * a.gate_stride + hq * kHeadDim + 4 * lane : nullptr;
+}
+
 // First page of workgroup w when P pages are shared by W workgroups.
 __device__ __forceinline__ int wg_start(int w, int P, int W) {
     return static_cast<int>(static_cast<int64_t>(w) * P / W);
@@ -465,11 +490,9 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
                 const float o3 = st.acc[g][3] * c0 + a1.w * c1;
                 if (whole) {
                     const float inv = 1.0f / l;
-                    uint2 o;
-                    o.x = pack_h2(o0 * inv, o1 * inv);
-                    o.y = pack_h2(o2 * inv, o3 * inv);
                     *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(c.b) * nh + h * G + g) * kHeadDim +
-                                               4 * lane) = o;
+                                               4 * lane) =
+                        out_fp16x4(o0 * inv, o1 * inv, o2 * inv, o3 * inv, gate_of(a, c.b, h * G + g, lane));
                 } else {
                     const size_t u = (static_cast<size_t>(slot) * hkv + h) * G + g;
                     *reinterpret_cast<float4 *>(a.ws_acc + u * kHeadDim + 4 * lane) = make_float4(o0, o1, o2, o3);
@@ -614,11 +637,9 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
         big = nb;
     }
     const float inv = 1.0f / lt;
-    uint2 o;
-    o.x = pack_h2(at.x * inv, at.y * inv);
-    o.y = pack_h2(at.z * inv, at.w * inv);
     *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(b) * a.num_heads + h * G + g) * kHeadDim +
-                               4 * lane) = o;
+                               4 * lane) =
+        out_fp16x4(at.x * inv, at.y * inv, at.z * inv, at.w * inv, gate_of(a, b, h * G + g, lane));
 }
 
 template <int G>

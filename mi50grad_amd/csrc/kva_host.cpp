@@ -791,7 +791,19 @@ static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_
     c->last_split = static_cast<int32_t>((pages * kva::kBlockTokens + a.n_wg - 1) / a.n_wg);
 }
 
-static int decode_impl(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
+// The output gate's layout: 8-byte aligned rows, a stride in whole 4-element
+// groups covering one sequence's H heads.
+static int check_gate(const void *gate, int64_t gate_stride, int32_t num_heads) {
+    if (!gate) return KVA_OK;
+    if (reinterpret_cast<uintptr_t>(gate) & 7u) return fail(KVA_ERR_MISALIGNED, "gate must be 8-byte aligned");
+    if (gate_stride % 4 != 0 || gate_stride < static_cast<int64_t>(num_heads) * kva::kHeadDim)
+        return fail(KVA_ERR_INVALID_ARG, "gate_stride %lld must be a multiple of 4 covering %d heads",
+                    static_cast<long long>(gate_stride), num_heads);
+    return KVA_OK;
+}
+
+static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *gate, int64_t gate_stride,
+                       void *out, kva_stream_t stream) {
     int rc = require_device(c);
     if (rc) return rc;
     if ((rc = check_layer(c, layer))) return rc;
@@ -799,7 +811,10 @@ static int decode_impl(kva_cache *c, int32_t layer, const void *q, void *out, kv
     if (!c->st_all_one) return fail(KVA_ERR_STATE, "kva_decode needs exactly one new token per sequence");
     if (!q || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (!aligned16(q) || !aligned16(out)) return fail(KVA_ERR_MISALIGNED, "q/out must be 16-byte aligned");
+    if ((rc = check_gate(gate, gate_stride, c->cfg.num_heads))) return rc;
     kva::DecodeArgs a{};
+    a.gate = static_cast<const uint16_t *>(gate);
+    a.gate_stride = gate_stride;
     a.q = static_cast<const uint16_t *>(q);
     a.k_pool = c->d_k + c->layer_elems * layer;
     a.v_pool = c->d_v + c->layer_elems * layer;
@@ -841,7 +856,15 @@ int kva_append_qknorm_rope(kva_cache *c, int32_t layer, void *q, void *k, const 
 int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
     int rc = capture_check(c, stream);
     if (rc) return capture_note(c, rc);
-    return capture_note(c, decode_impl(c, layer, q, out, stream));
+    return capture_note(c, decode_impl(c, layer, q, nullptr, 0, out, stream));
+}
+
+int kva_decode_gated(kva_cache *c, int32_t layer, const void *q, const void *gate, int64_t gate_stride,
+                     void *out, kva_stream_t stream) {
+    int rc = capture_check(c, stream);
+    if (rc) return capture_note(c, rc);
+    if (!gate) return capture_note(c, fail(KVA_ERR_INVALID_ARG, "NULL gate"));
+    return capture_note(c, decode_impl(c, layer, q, gate, gate_stride, out, stream));
 }
 
 static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream,
@@ -1074,7 +1097,7 @@ int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row, const vo
     return KVA_OK;
 }
 
-static int legacy_decode(kva_cache *ws, const void *q, const void *k_base, const void *v_base,
+static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const void *k_base, const void *v_base,
                          void *out, int32_t kv_seq_len, int32_t batch, int64_t batch_stride,
                          int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream) {
     if (!q || !k_base || !v_base || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
@@ -1093,7 +1116,10 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *k_base, const
         return fail(KVA_ERR_INVALID_ARG, "batch_stride %lld must be a multiple of 16 covering %d rows",
                     static_cast<long long>(batch_stride), kv_seq_len);
     if (ws && ws->host_only) return fail(KVA_ERR_NO_DEVICE, "workspace cache is host-only");
+    if (int rc = check_gate(gate, static_cast<int64_t>(num_heads) * kva::kHeadDim, num_heads)) return rc;
     kva::DecodeArgs a{};
+    a.gate = static_cast<const uint16_t *>(gate);
+    a.gate_stride = static_cast<int64_t>(num_heads) * kva::kHeadDim;
     a.q = static_cast<const uint16_t *>(q);
     a.k_pool = static_cast<const uint16_t *>(k_base);
     a.v_pool = static_cast<const uint16_t *>(v_base);
@@ -1120,14 +1146,21 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *k_base, const
 int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base, const void *v_base,
                       void *out, int32_t kv_seq_len, int32_t num_heads, int32_t num_kv_heads,
                       kva_stream_t stream) {
-    return legacy_decode(ws, q, k_base, v_base, out, kv_seq_len, 1, 0, num_heads, num_kv_heads, stream);
+    return legacy_decode(ws, q, nullptr, k_base, v_base, out, kv_seq_len, 1, 0, num_heads, num_kv_heads, stream);
 }
 
 int kva_legacy_decode_batched(kva_cache *ws, const void *q, const void *k_base, const void *v_base,
                               void *out, int32_t kv_seq_len, int32_t batch, int64_t batch_stride,
                               int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream) {
-    return legacy_decode(ws, q, k_base, v_base, out, kv_seq_len, batch, batch_stride, num_heads,
+    return legacy_decode(ws, q, nullptr, k_base, v_base, out, kv_seq_len, batch, batch_stride, num_heads,
                          num_kv_heads, stream);
+}
+
+int kva_legacy_decode_gated(kva_cache *ws, const void *q, const void *gate, const void *k_base,
+                            const void *v_base, void *out, int32_t kv_seq_len, int32_t num_heads,
+                            int32_t num_kv_heads, kva_stream_t stream) {
+    if (!gate) return fail(KVA_ERR_INVALID_ARG, "NULL gate");
+    return legacy_decode(ws, q, gate, k_base, v_base, out, kv_seq_len, 1, 0, num_heads, num_kv_heads, stream);
 }
 
 int kva_hbm_copy(void *dst, const void *src, size_t bytes, kva_stream_t stream) {

@@ -81,6 +81,10 @@ struct DecodeArgs {
                               // sequence is whole in one workgroup (no combine)
     float *ws_ml;             // [2*n_wg][Hkv][G][2]
     uint16_t *out;            // [n_seqs][H][256]
+    // Output gate (null = none): out = fp16(fp16(attn) * sigmoid(gate)), the
+    // gate row of sequence b, query head hq at gate + b*gate_stride + hq*256.
+    const uint16_t *gate;
+    int64_t gate_stride;
 };
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
 

@@ -146,8 +146,14 @@ class PagedKVCache:
         _lib.call("kva_append_qknorm_rope", self.handle, layer, _ptr(q), _ptr(k), _ptr(v),
                   _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab), table_rows, stream)
 
-    def decode(self, layer: int, q, out, stream=None) -> None:
-        _lib.call("kva_decode", self.handle, layer, _ptr(q), _ptr(out), stream)
+    def decode(self, layer: int, q, out, stream=None, gate=None, gate_stride: int = 0) -> None:
+        """Decode attention; with `gate`, the output gate (out *= sigmoid(gate),
+        sigmoid_mul.hip) is applied in the same launch."""
+        if gate is None:
+            _lib.call("kva_decode", self.handle, layer, _ptr(q), _ptr(out), stream)
+        else:
+            stride = gate_stride or self.num_heads * 256
+            _lib.call("kva_decode_gated", self.handle, layer, _ptr(q), _ptr(gate), stride, _ptr(out), stream)
 
     def prefill(self, layer: int, q, out, stream=None) -> None:
         _lib.call("kva_prefill", self.handle, layer, _ptr(q), _ptr(out), stream)

@@ -189,6 +189,18 @@ def decode_attention(q: np.ndarray, ks, vs) -> np.ndarray:
     return np.stack([attention_fp32(q[b:b + 1], ks[b], vs[b])[0] for b in range(len(ks))])
 
 
+def sigmoid_gate(out: np.ndarray, gate: np.ndarray) -> np.ndarray:
+    """The attention output gate, sigmoid_mul.hip:10-22 as used after decode
+    at engine.py:2055-2056: each fp16 output element times sigmoid of the
+    matching fp16 gate element (the gate half of the fused [Q | Q_gate]
+    projection, engine.py:1069-1071), in float32, rounded to fp16:
+    ``fp16(float(out) * (1 / (1 + exp(-float(gate)))))``."""
+    o = np.asarray(out, np.float16).astype(np.float32)
+    g = np.asarray(gate, np.float16).astype(np.float32)
+    sig = np.float32(1.0) / (np.float32(1.0) + np.exp(-g, dtype=np.float32))
+    return (o * sig).astype(np.float16)
+
+
 def chunk_visibility(prefix_len: int, chunk_len: int) -> np.ndarray:
     """Causal rule for a chunk appended after ``prefix_len`` cached rows.
 

@@ -325,3 +325,22 @@ def test_planted_mistakes_are_caught():
     g = golden()
     swapped = orc.tree_visibility_cache_order(g["tree3_parents"], g["tree3_kv_len"]).astype(int)
     assert swapped.tolist() != g["tree3_rows"]
+
+
+def test_sigmoid_gate_pins():
+    """sigmoid_mul.hip:10-22 restated: closed-form gates, the sigmoid's
+    symmetry, and a float64 computation within one fp16 rounding."""
+    rng = np.random.default_rng(9)
+    out = (rng.standard_normal(4096) * 3).astype(np.float16)
+    out = out[np.abs(out.astype(np.float32)) > 1e-3]  # normal range: halving is exact
+    z = np.zeros_like(out)
+    assert np.array_equal(orc.sigmoid_gate(out, z).view(np.uint16), (out / np.float16(2)).view(np.uint16))
+    assert np.array_equal(orc.sigmoid_gate(out, z + np.float16(20)).view(np.uint16), out.view(np.uint16))
+    assert np.all(orc.sigmoid_gate(out, z - np.float16(20)).astype(np.float32) == 0)
+    g = (rng.standard_normal(out.shape) * 2).astype(np.float16)
+    both = orc.sigmoid_gate(out, g).astype(np.float32) + orc.sigmoid_gate(out, -g).astype(np.float32)
+    ulp = np.abs(out.astype(np.float32)) * 2.0 ** -10
+    assert np.all(np.abs(both - out.astype(np.float32)) <= 2 * ulp + 1e-7)
+    ref = (out.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))).astype(np.float16)
+    diff = np.abs(orc.sigmoid_gate(out, g).astype(np.float64) - ref.astype(np.float64))
+    assert np.all(diff <= np.abs(ref.astype(np.float64)) * 2.0 ** -10 + 1e-7)
