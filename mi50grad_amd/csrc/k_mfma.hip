@@ -70,12 +70,22 @@ struct BlockPages {
     int p0, p1;
 };
 
+// Scalar loads: waiting for a page id then never drains the K/V loads in
+// flight (a vector load + readfirstlane would wait for every older load).
 __device__ __forceinline__ BlockPages block_pages(const int32_t *trow, int blk, int ctx) {
     const int pg = 2 * blk;
     BlockPages bp;
-    bp.p0 = __builtin_amdgcn_readfirstlane(trow[pg]);
-    bp.p1 = (pg + 1) * kBlockTokens < ctx ? __builtin_amdgcn_readfirstlane(trow[pg + 1]) : bp.p0;
+    bp.p0 = ld_uniform(trow + pg);
+    bp.p1 = (pg + 1) * kBlockTokens < ctx ? ld_uniform(trow + pg + 1) : bp.p0;
     return bp;
+}
+
+// Every lane issues every load of a stage (a key past the sequence, or a
+// chunk beyond the block, reads the block's first key and is zeroed after):
+// with the same loads on every path the compiler's load counters stay exact,
+// so waiting for one stage never drains the next one in flight.
+__device__ __forceinline__ uint4 zero_unless(bool keep, uint4 x) {
+    return keep ? x : make_uint4(0, 0, 0, 0);
 }
 
 template <int NT>
@@ -88,30 +98,27 @@ __device__ __forceinline__ void stage_load(Stage<NT> &st, const MultiQueryArgs &
     for (int i = 0; i < Stage<NT>::kPerK; ++i) {
         const int c = tid + i * NT;
         const int kk = c >> 5;
-        if (c < kMqKeys * 32 && key0 + kk < ctx) {
-            const int page = kk < 16 ? bp.p0 : bp.p1;
-            const size_t off = (static_cast<size_t>(page) * kBlockTokens + (kk & 15)) * row_elems + head_off +
-                               (c & 31) * 8;
-            st.k[i] = ld16(a.k_pool + off);
-        } else {
-            st.k[i] = make_uint4(0, 0, 0, 0);
-        }
+        const bool ok = c < kMqKeys * 32 && key0 + kk < ctx;
+        const int kr = ok ? kk : 0;
+        const int page = kr < 16 ? bp.p0 : bp.p1;
+        const size_t off = (static_cast<size_t>(page) * kBlockTokens + (kr & 15)) * row_elems + head_off +
+                           (ok ? (c & 31) * 8 : 0);
+        st.k[i] = zero_unless(ok, ld16(a.k_pool + off));
     }
 #pragma unroll
     for (int i = 0; i < Stage<NT>::kPerV; ++i) {
         const int v = tid + i * NT;
-        const int kg = v >> 5;
-        const int col = (v & 31) * 8;
+        const bool vin = v < kMqKeys / 4 * 32;
+        const int kg = vin ? v >> 5 : 0;
+        const int col = vin ? (v & 31) * 8 : 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int kk = 4 * kg + e;
-            if (v < kMqKeys / 4 * 32 && key0 + kk < ctx) {
-                const int page = kk < 16 ? bp.p0 : bp.p1;
-                st.v[i][e] = ld16(a.v_pool + (static_cast<size_t>(page) * kBlockTokens + (kk & 15)) * row_elems +
-                                  head_off + col);
-            } else {
-                st.v[i][e] = make_uint4(0, 0, 0, 0);
-            }
+            const bool ok = vin && key0 + kk < ctx;
+            const int kr = ok ? kk : 0;
+            const int page = kr < 16 ? bp.p0 : bp.p1;
+            st.v[i][e] = zero_unless(ok, ld16(a.v_pool + (static_cast<size_t>(page) * kBlockTokens + (kr & 15)) *
+                                                             row_elems + head_off + col));
         }
     }
 }
@@ -169,8 +176,10 @@ __global__ __launch_bounds__(64 * G) void mq_kernel(MultiQueryArgs a) {
     const int nh = a.num_heads;
     const float scale = kLog2e / 16.0f;
 
-    __shared__ uint16_t k_lds[kMqKeys * kKRow];
-    __shared__ uint16_t vt_lds[kHeadDim * kVRow];
+    // Two LDS tiles: block blk+1 is stored into one while block blk is read
+    // from the other, so one barrier per block separates them.
+    __shared__ uint16_t k_lds2[2][kMqKeys * kKRow];
+    __shared__ uint16_t vt_lds2[2][kHeadDim * kVRow];
 
     int u = upper_index(a.mq_pre, a.n_units, q0);
     int p = q0;
@@ -211,21 +220,39 @@ __global__ __launch_bounds__(64 * G) void mq_kernel(MultiQueryArgs a) {
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) acc[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-        // Pipeline: block blk+1's K/V loads and block blk+2's page ids are in
-        // flight while block blk is computed from LDS.
-        Stage<NT> stg;
+        // Pipeline: two register stages, so blocks blk+1 and blk+2's K/V loads
+        // (64 KB per workgroup) are in flight while block blk is computed from
+        // LDS; the stage just stored is refilled with block blk+2 at once.
+        // Loads past the segment repeat its last block (same loads on every
+        // path, no use).
+        // (A 64-thread workgroup, G = 1, holds a whole block per thread: one
+        // stage.)
+        constexpr int kAhead = G >= 2 ? 2 : 1;
+        Stage<NT> stg[kAhead];
         const int blk0 = p - ub;
         const int blk1 = seg_end - ub;
-        stage_load<NT>(stg, a, block_pages(trow, blk0, ctx), h, blk0 * kMqKeys, ctx);
-        BlockPages nxt = block_pages(trow, blk0 + 1 < blk1 ? blk0 + 1 : blk0, ctx);
-        for (int blk = blk0; blk < blk1; ++blk) {
-            __syncthreads();  // previous block's LDS reads are done
-            stage_store<NT>(stg, k_lds, vt_lds);
-            __syncthreads();
+        const int blast = blk1 - 1;
+        stage_load<NT>(stg[0], a, block_pages(trow, blk0, ctx), h, blk0 * kMqKeys, ctx);
+        if constexpr (kAhead == 2)
+            stage_load<NT>(stg[1], a, block_pages(trow, min(blk0 + 1, blast), ctx), h,
+                           min(blk0 + 1, blast) * kMqKeys, ctx);
+        // Block blk0 to tile 0 now; its stage then fetches block blk0+kAhead.
+        // (The previous segment ended on a barrier after its last reads.)
+        stage_store<NT>(stg[0], k_lds2[0], vt_lds2[0]);
+        stage_load<NT>(stg[0], a, block_pages(trow, min(blk0 + kAhead, blast), ctx), h,
+                       min(blk0 + kAhead, blast) * kMqKeys, ctx);
+        BlockPages nxt = block_pages(trow, min(blk0 + kAhead + 1, blast), ctx);
+        __syncthreads();
+        // One block: `cur` holds block blk+1; it goes to the other tile and
+        // then fetches block blk+1+kAhead, while block blk is computed.
+        auto do_block = [&](Stage<NT> &cur, int blk) {
             if (blk + 1 < blk1) {
-                stage_load<NT>(stg, a, nxt, h, (blk + 1) * kMqKeys, ctx);
-                nxt = block_pages(trow, blk + 2 < blk1 ? blk + 2 : blk + 1, ctx);
+                stage_store<NT>(cur, k_lds2[(blk + 1 - blk0) & 1], vt_lds2[(blk + 1 - blk0) & 1]);
+                stage_load<NT>(cur, a, nxt, h, min(blk + 1 + kAhead, blast) * kMqKeys, ctx);
+                nxt = block_pages(trow, min(blk + 2 + kAhead, blast), ctx);
             }
+            const uint16_t *k_lds = k_lds2[(blk - blk0) & 1];  // block blk0 went to tile 0
+            const uint16_t *vt_lds = vt_lds2[(blk - blk0) & 1];
             const int key0 = blk * kMqKeys;
 
             // S^T for keys key0 + 16*nt + 4*grp + i, query column `col`.
@@ -281,6 +308,12 @@ __global__ __launch_bounds__(64 * G) void mq_kernel(MultiQueryArgs a) {
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     __builtin_bit_cast(half8_t, make_uint4(v0.x, v0.y, v1.x, v1.y)), pb, acc[dt], 0, 0, 0);
             }
+            __syncthreads();  // every wave is done with this tile and the next one is stored
+        };
+        for (int blk = blk0; blk < blk1; blk += 2) {
+            do_block(stg[kAhead - 1], blk);
+            if (blk + 1 >= blk1) break;
+            do_block(stg[0], blk + 1);
         }
 
         // The four lane groups hold disjoint keys of each query column.
