@@ -9,20 +9,33 @@
 //   tree:  keys [0, len_before) and the new tokens in its tree bit set
 //       (flash_attn_tree.hip:72-175 under tree_attention.py:186-208).
 //
-// Unit = (sequence, tile of 16 new tokens, kv head); a 64*G-thread workgroup
-// runs one wave per query head of the GQA group, so every K/V block staged
-// in LDS serves G heads.  Work is split stream-K over 32-key blocks: the
-// blocks of all units are laid end to end and each workgroup takes an equal
-// share; units cut by a share boundary leave partials for mq_combine_kernel.
+// Unit = (sequence, tile of Q new tokens, kv head).  The tile's query rows
+// are the Q x G (token, query head) pairs of the GQA group packed row after
+// row — every head of the group attends to the same K/V — so four waves of
+// 16 x NT rows each (Q = 64*NT/G) leave at most G-1 rows idle (the tree
+// verify's 9 nodes x 6 heads fill 54 of 64 rows).  Work is split stream-K
+// over 32-key blocks: the blocks of all units are laid end to end and each
+// workgroup takes an equal share; units cut by a share boundary leave
+// partials for mq_combine_kernel.
 //
-// Per 32-key block and wave (v_mfma_f32_16x16x32_f16, C layout: lane l holds
-// rows 4*(l/16)+i, column l%16):
-//   S^T[key][q] = K[key][:] . Q[q][:]   (A = K rows from LDS, B = Q^T held
-//       in registers for the whole unit; 2 key tiles x 8 k-steps);
-//   per query column: scale, mask, online softmax (max over the 4 lane
-//       groups with two shuffles), P^T in fp16 — already the B operand of
-//   O^T[dim][q] += V^T[dim][key] . P^T[key][q]   (A = V^T from LDS, stored
-//       transposed when staged; 16 dim tiles).
+// K/V blocks travel HBM -> LDS by buffer loads that write LDS directly (no
+// register staging), through a ring of four 32 KB stages: while block i is
+// computed, blocks i+1..i+3 (96 KB) are in flight.  Each wave issues the
+// loads of 8 keys of every block; a wave waits for its own loads of block i
+// (vmcnt) and one workgroup barrier makes all of them visible and frees the
+// stage of block i-1 for block i+3.  Rows are stored with an XOR swizzle of
+// their 16-byte granules so both read patterns below are conflict-free.
+//
+// Per block, wave and 16-row tile t (v_mfma_f32_16x16x32_f16, C layout:
+// lane l holds rows 4*(l/16)+i, column l%16):
+//   S^T[key][row] = K[key][:] . Q[row][:]   (A = K rows read from LDS once
+//       for all NT tiles, B = Q^T held in registers for the whole unit);
+//   per row: scale, mask, online softmax (max over the 4 lane groups with
+//       two permlane swaps; the reference max moves, and acc is rescaled,
+//       only when a block's max passes it by more than a slack), P^T in
+//       fp16 — already the B operand of
+//   O^T[dim][row] += V^T[dim][key] . P^T[key][row]   (A = V^T read with
+//       ds_read_b64_tr_b16 from the row-major V tile; 16 dim tiles).
 // The k-index permutation of P^T (keys 4g..4g+3 and 16+4g..16+4g+3 in lane
 // group g) is matched by the V^T reads, so the sum is over the right pairs.
 #include "k_common.h"
@@ -31,9 +44,16 @@
 namespace kva {
 namespace {
 
-constexpr int kKRow = kHeadDim + 8;  // K tile row stride (halves): 528 B, conflict-free b128 reads
-constexpr int kVRow = kMqKeys + 8;   // V^T tile row stride (halves): 80 B
+constexpr int kWaves = 4;
+constexpr int kRing = 4;                            // LDS stages
+constexpr int kTileBytes = kMqKeys * kHeadDim * 2;  // 16 KB: K or V of a block
+constexpr int kRowBytes = kHeadDim * 2;             // 512 B: one key of one head
+constexpr int kDmaPerWave = 8;                      // 4 K + 4 V loads per block
 constexpr float kLog2e = 1.4426950408889634f;
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 __device__ __forceinline__ int mq_wg_start(int w, int n, int W) {
     return static_cast<int>(static_cast<int64_t>(w) * n / W);
@@ -43,319 +63,399 @@ __device__ __forceinline__ int mq_wg_of(int p, int n, int W) {
     while (w + 1 < W && mq_wg_start(w + 1, n, W) <= p) ++w;
     return w;
 }
-// Largest i in [0, n) with pre[i] <= x (pre non-decreasing, pre[0] <= x).
+// Largest i in [0, n) with pre[i] <= x (pre non-decreasing, pre[0] <= x);
+// wave-uniform arguments, scalar loads.
 __device__ __forceinline__ int upper_index(const int32_t *pre, int n, int x) {
     int lo = 0, hi = n - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (pre[mid] <= x) lo = mid; else hi = mid - 1;
+        if (ld_uniform(pre + mid) <= x) lo = mid; else hi = mid - 1;
     }
     return lo;
 }
 
-// Staged 32-key block.  K: 1024 chunks of 16 bytes (key = c/32, dims
-// 8*(c%32)..+8) spread over the threads.  V: 256 tasks of 4 keys x 8 dims
-// (keys 4*(v/32).., dims 8*(v%32)..), transposed in registers so each dim's
-// 4 keys are stored to V^T with one 8-byte write.
-template <int NT>
-struct Stage {
-    static constexpr int kPerK = (kMqKeys * 32 + NT - 1) / NT;
-    static constexpr int kPerV = (kMqKeys / 4 * 32 + NT - 1) / NT;
-    uint4 k[kPerK];
-    uint4 v[kPerV][4];
+// Swizzled 16-byte granule of a 512-byte key row in LDS (key = key index
+// within the block).  K reads take 16 consecutive keys at one granule, V^T
+// reads 4 consecutive keys at two neighbouring granules.
+__device__ __forceinline__ int k_granule(int key, int p) { return p ^ (key & 15); }
+__device__ __forceinline__ int v_granule(int key, int p) { return p ^ ((key & 7) << 1); }
+
+// The facts of one unit (all wave-uniform, read by scalar loads).
+struct Unit {
+    int u, ub, ue;        // unit index and its global block range [ub, ue)
+    int b, h, tile;       // sequence (index in the step), kv head, query tile
+    int ctx, ns, tok, T;  // keys visible, first new slot, first token, new tokens
+    const int32_t *trow;  // block-table row
 };
 
-// Page ids of a block's two 16-key pages (wave-uniform scalars).
-struct BlockPages {
-    int p0, p1;
-};
-
-// Scalar loads: waiting for a page id then never drains the K/V loads in
-// flight (a vector load + readfirstlane would wait for every older load).
-__device__ __forceinline__ BlockPages block_pages(const int32_t *trow, int blk, int ctx) {
-    const int pg = 2 * blk;
-    BlockPages bp;
-    bp.p0 = ld_uniform(trow + pg);
-    bp.p1 = (pg + 1) * kBlockTokens < ctx ? ld_uniform(trow + pg + 1) : bp.p0;
-    return bp;
+__device__ __forceinline__ Unit load_unit(const MultiQueryArgs &a, int u, int b) {
+    Unit x;
+    x.u = u;
+    x.ub = ld_uniform(a.mq_pre + u);
+    x.ue = ld_uniform(a.mq_pre + u + 1);
+    while (ld_uniform(a.upre + b + 1) <= u) ++b;  // units are in sequence order
+    x.b = b;
+    const int r = u - ld_uniform(a.upre + b);
+    x.tile = r / a.num_kv_heads;
+    x.h = r - x.tile * a.num_kv_heads;
+    x.ctx = ld_uniform(a.ctx_lens + b);
+    x.ns = ld_uniform(a.new_start + b);
+    x.tok = ld_uniform(a.tok_off + b);
+    x.T = ld_uniform(a.tok_off + b + 1) - x.tok;
+    x.trow = a.table + static_cast<size_t>(ld_uniform(a.seq_ids + b)) * a.table_stride;
+    return x;
 }
 
-// Every lane issues every load of a stage (a key past the sequence, or a
-// chunk beyond the block, reads the block's first key and is zeroed after):
-// with the same loads on every path the compiler's load counters stay exact,
-// so waiting for one stage never drains the next one in flight.
-__device__ __forceinline__ uint4 zero_unless(bool keep, uint4 x) {
-    return keep ? x : make_uint4(0, 0, 0, 0);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t pool_rsrc(const uint16_t *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
 }
 
-template <int NT>
-__device__ __forceinline__ void stage_load(Stage<NT> &st, const MultiQueryArgs &a, BlockPages bp,
-                                           int h, int key0, int ctx) {
-    const int tid = threadIdx.x;
-    const size_t row_elems = static_cast<size_t>(a.num_kv_heads) * kHeadDim;
-    const size_t head_off = static_cast<size_t>(h) * kHeadDim;
+// LDS byte address of a __shared__ location.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t *)p));
+}
+
+// One 16-byte-per-lane buffer load written straight to LDS: lane l's bytes
+// go to lds + 16*l.  Written as inline assembly on purpose: the compiler
+// would otherwise order every later LDS read of the kernel behind all such
+// loads in flight (it cannot tell the ring's stages apart), which would
+// drain the ring at every block.  The kernel does its own waiting
+// (wait_block + barrier); to the compiler these loads are invisible, so its
+// own load waits can only grow stricter, never too weak.
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(lds), "v"(voff), "s"(r)
+        : "memory", "m0");
+}
+
+// Issue this wave's share of block g of unit un into LDS stage `st`: keys
+// 8*wv..8*wv+7 of the block (one page), K and V, four 1 KB loads each (lane
+// l writes granule l%32 of key 2i + l/32).  Keys past the sequence read its
+// last key (finite data; the mask drops them).  A disabled issue (past the
+// workgroup's share) goes through an empty resource: no memory access, but
+// the same loads, so every wave's load counter advances alike.
+__device__ __forceinline__ void issue_block(uint8_t *st, const MultiQueryArgs &a, const Unit &un, int g, bool on,
+                                            int wv, int lane, int row_bytes) {
+    const int key0 = (g - un.ub) * kMqKeys + 8 * wv;  // key of the unit
+    const int last = un.ctx - 1;
+    const int page = on ? ld_uniform(un.trow + (min(key0, last) >> 4)) : 0;
+    const size_t off = (static_cast<size_t>(page) * kBlockTokens * row_bytes + un.h * kRowBytes) / 2;
+    const uint32_t n = on ? kBlockTokens * row_bytes : 0u;
+    const auto rk = pool_rsrc(a.k_pool + off, n), rv = pool_rsrc(a.v_pool + off, n);
+    const int q = lane & 31;
 #pragma unroll
-    for (int i = 0; i < Stage<NT>::kPerK; ++i) {
-        const int c = tid + i * NT;
-        const int kk = c >> 5;
-        const bool ok = c < kMqKeys * 32 && key0 + kk < ctx;
-        const int kr = ok ? kk : 0;
-        const int page = kr < 16 ? bp.p0 : bp.p1;
-        const size_t off = (static_cast<size_t>(page) * kBlockTokens + (kr & 15)) * row_elems + head_off +
-                           (ok ? (c & 31) * 8 : 0);
-        st.k[i] = zero_unless(ok, ld16(a.k_pool + off));
-    }
-#pragma unroll
-    for (int i = 0; i < Stage<NT>::kPerV; ++i) {
-        const int v = tid + i * NT;
-        const bool vin = v < kMqKeys / 4 * 32;
-        const int kg = vin ? v >> 5 : 0;
-        const int col = vin ? (v & 31) * 8 : 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int kk = 4 * kg + e;
-            const bool ok = vin && key0 + kk < ctx;
-            const int kr = ok ? kk : 0;
-            const int page = kr < 16 ? bp.p0 : bp.p1;
-            st.v[i][e] = zero_unless(ok, ld16(a.v_pool + (static_cast<size_t>(page) * kBlockTokens + (kr & 15)) *
-                                                             row_elems + head_off + col));
-        }
+    for (int i = 0; i < 4; ++i) {
+        const int kl = 8 * wv + 2 * i + (lane >> 5);  // key within the block
+        const int row = min(key0 + 2 * i + (lane >> 5), last) & 15;
+        const uint32_t dst = lds_addr(st + (8 * wv + 2 * i) * kRowBytes);  // keys 8wv+2i, +1: this load's 1 KB
+        load_to_lds(rk, dst, row * row_bytes + 16 * k_granule(kl, q));
+        load_to_lds(rv, dst + kTileBytes, row * row_bytes + 16 * v_granule(kl, q));
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void stage_store(const Stage<NT> &st, uint16_t *k_lds, uint16_t *vt_lds) {
-    const int tid = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < Stage<NT>::kPerK; ++i) {
-        const int c = tid + i * NT;
-        if (c < kMqKeys * 32)
-            *reinterpret_cast<uint4 *>(k_lds + (c >> 5) * kKRow + (c & 31) * 8) = st.k[i];
-    }
-#pragma unroll
-    for (int i = 0; i < Stage<NT>::kPerV; ++i) {
-        const int v = tid + i * NT;
-        if (v < kMqKeys / 4 * 32) {
-            const int key = 4 * (v >> 5);
-            const int col = (v & 31) * 8;
-            // word w of key e holds dims col+2w, col+2w+1
-            const uint32_t w0[4] = {st.v[i][0].x, st.v[i][0].y, st.v[i][0].z, st.v[i][0].w};
-            const uint32_t w1[4] = {st.v[i][1].x, st.v[i][1].y, st.v[i][1].z, st.v[i][1].w};
-            const uint32_t w2[4] = {st.v[i][2].x, st.v[i][2].y, st.v[i][2].z, st.v[i][2].w};
-            const uint32_t w3[4] = {st.v[i][3].x, st.v[i][3].y, st.v[i][3].z, st.v[i][3].w};
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint2 lo, hi;  // dims col+2w (low halves) and col+2w+1 (high halves), keys key..key+3
-                lo.x = (w0[w] & 0xffffu) | (w1[w] << 16);
-                lo.y = (w2[w] & 0xffffu) | (w3[w] << 16);
-                hi.x = (w0[w] >> 16) | (w1[w] & 0xffff0000u);
-                hi.y = (w2[w] >> 16) | (w3[w] & 0xffff0000u);
-                *reinterpret_cast<uint2 *>(vt_lds + (col + 2 * w) * kVRow + key) = lo;
-                *reinterpret_cast<uint2 *>(vt_lds + (col + 2 * w + 1) * kVRow + key) = hi;
-            }
-        }
-    }
+// Wait until at most kDmaPerWave * (kRing - 2) of this wave's loads are
+// outstanding (loads complete in order): block i's have landed in LDS while
+// blocks i+1 and i+2 may still be in flight.
+__device__ __forceinline__ void wait_block() {
+    constexpr int n = kDmaPerWave * (kRing - 2);
+    // s_waitcnt fields: vmcnt[3:0], expcnt[6:4] (7 = no wait), lgkmcnt[11:8]
+    // (15 = no wait), vmcnt[5:4] in bits [15:14].
+    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
 }
 
 __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
-template <int G>
-__global__ __launch_bounds__(64 * G) void mq_kernel(MultiQueryArgs a) {
-    constexpr int NT = 64 * G;
+// Max / sum over the four 16-lane groups (every lane gets it): permlane
+// swaps, VALU only (no LDS round trip).  v_permlane16_swap with both
+// operands holding x leaves x of rows 0,0,2,2 in the first and of rows
+// 1,1,3,3 in the second register; v_permlane32_swap likewise pairs the
+// halves, so combining the two registers after each covers all four.
+// Inline assembly: with one value in both operands the compiler's builtin
+// has been seen to read the first result twice.
+__device__ __forceinline__ void swap16(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float group4_max(float x) {
+    float a = x, b = x;
+    swap16(a, b);
+    a = fmaxf(a, b);
+    b = a;
+    swap32(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float group4_sum(float x) {
+    float a = x, b = x;
+    swap16(a, b);
+    a += b;
+    b = a;
+    swap32(a, b);
+    return a + b;
+}
+
+// A row's reference max moves only when a block's max exceeds it by more
+// than this (log2 units): probabilities then stay below 2^8 (fp16 holds
+// them to the same relative precision) and the accumulators are rescaled
+// only on such jumps, not at every block where some row's max grew.
+constexpr float kRescaleSlack = 8.0f;
+
+template <int NT, bool TREE>
+__global__ __launch_bounds__(64 * kWaves) void mq_kernel(MultiQueryArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kRing][2 * kTileBytes];
     const int w = blockIdx.x;
     const int W = a.n_wg;
     const int NB = a.total_blocks;
     const int q0 = mq_wg_start(w, NB, W);
     const int q1 = mq_wg_start(w + 1, NB, W);
     if (q0 >= q1) return;  // uniform over the workgroup
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head within the group
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int col = lane & 15;   // query row of the tile (C/B column)
-    const int grp = lane >> 4;   // lane group: keys 4*grp.. of a 16-key tile
+    const int col = lane & 15;  // this lane's row within each 16-row tile (C/B column)
+    const int grp = lane >> 4;  // lane group: keys 4*grp.. of a 16-key tile
     const int hkv = a.num_kv_heads;
     const int nh = a.num_heads;
+    const int G = nh / hkv;
+    const int Q = a.q_tile;
+    const int row_bytes = hkv * kRowBytes;
     const float scale = kLog2e / 16.0f;
 
-    // Two LDS tiles: block blk+1 is stored into one while block blk is read
-    // from the other, so one barrier per block separates them.
-    __shared__ uint16_t k_lds2[2][kMqKeys * kKRow];
-    __shared__ uint16_t vt_lds2[2][kHeadDim * kVRow];
+    // This lane's query row in each of the wave's NT tiles: (token iq, head gq).
+    int iq[NT], gq[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int rho = 16 * (wv * NT + t) + col;
+        iq[t] = rho / G;
+        gq[t] = rho - iq[t] * G;
+    }
 
-    int u = upper_index(a.mq_pre, a.n_units, q0);
-    int p = q0;
+    // Issue side: the unit and block of the next load, kRing-1 blocks ahead
+    // of the compute side, across unit boundaries.
+    const int u0 = upper_index(a.mq_pre, a.n_units, q0);
+    Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0));
+    int ig = q0;
+    auto issue = [&](int slot) {
+        const bool on = ig < q1;
+        issue_block(ring[slot], a, iu, ig, on, wv, lane, row_bytes);
+        if (on && ++ig < q1 && ig >= iu.ue) iu = load_unit(a, iu.u + 1, iu.b);
+    };
+    Unit cu = iu;
+#pragma unroll
+    for (int s = 0; s + 1 < kRing; ++s) issue(s);
+
+    int n_done = 0;  // blocks computed by this workgroup (ring position)
+    int g = q0;
     bool first_seg = true;
-    while (p < q1) {
-        const int ub = a.mq_pre[u];
-        const int ue = a.mq_pre[u + 1];
-        if (p >= ue) {  // empty or finished unit
-            ++u;
-            continue;
-        }
-        const int b = upper_index(a.upre, a.n_seqs, u);
-        const int x = u - a.upre[b];
-        const int tile = x / hkv;
-        const int h = x - tile * hkv;
-        const int seg_end = min(ue, q1);
-        const int tok_base = a.tok_off[b];
-        const int T = a.tok_off[b + 1] - tok_base;
-        const int ns = a.new_start[b];
-        const int ctx = a.ctx_lens[b];
-        const int32_t *trow = a.table + static_cast<size_t>(a.seq_ids[b]) * a.table_stride;
-
-        // This lane's query row (token qi of the sequence's new tokens).
-        const int qi = tile * kMqRows + col;
-        const bool qvalid = qi < T;
-        const int qslot = ns + qi;
-        const uint64_t qbits = (a.tree && qvalid) ? a.tok_bits[tok_base + qi] : 0ull;
-        uint4 qb[8];  // B operand Q^T: dims 32*kk + 8*grp .. +8 of query qi, head h*G+wave
-        {
-            const uint16_t *qr = a.q + (static_cast<size_t>(tok_base + (qvalid ? qi : 0)) * nh + h * G + wave) * kHeadDim;
+    while (true) {
+        const int seg_end = min(cu.ue, q1);
+        const bool whole = g == cu.ub && seg_end == cu.ue;
+        // Query rows of this unit.
+        bool qvalid[NT];
+        int qslot[NT];
+        uint64_t qbits[NT];
+        uint4 qb[NT][8];  // B operand Q^T: dims 32*kk + 8*grp .. +8
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int qi = cu.tile * Q + iq[t];
+            qvalid[t] = iq[t] < Q && qi < cu.T;
+            qslot[t] = cu.ns + qi;
+            qbits[t] = (TREE && qvalid[t]) ? a.tok_bits[cu.tok + qi] : 0ull;
+            const uint16_t *qr =
+                a.q + (static_cast<size_t>(cu.tok + (qvalid[t] ? qi : 0)) * nh + cu.h * G + gq[t]) * kHeadDim;
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk)
-                qb[kk] = qvalid ? ld16(qr + 32 * kk + 8 * grp) : make_uint4(0, 0, 0, 0);
+                qb[t][kk] = qvalid[t] ? ld16(qr + 32 * kk + 8 * grp) : make_uint4(0, 0, 0, 0);
+        }
+        // Take delivery of the query rows here, once per unit: left to the
+        // compiler, the wait for them would sit inside the block loop and
+        // (not seeing the LDS loads) drain the ring at every block.
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            asm volatile("" : "+v"(qbits[t]));
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk)
+                asm volatile("" : "+v"(qb[t][kk].x), "+v"(qb[t][kk].y), "+v"(qb[t][kk].z), "+v"(qb[t][kk].w));
+        }
+        float m[NT], l[NT];
+        float4_t acc[NT][16];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            m[t] = -INFINITY;
+            l[t] = 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < 16; ++dt) acc[t][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
         }
 
-        float m = -INFINITY, l = 0.0f;
-        float4_t acc[16];
-#pragma unroll
-        for (int dt = 0; dt < 16; ++dt) acc[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (; g < seg_end; ++g) {
+            wait_block();
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            issue((n_done + kRing - 1) % kRing);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint8_t *kt = ring[n_done % kRing];
+            const uint8_t *vt = kt + kTileBytes;
+            const int key0 = (g - cu.ub) * kMqKeys;
 
-        // Pipeline: two register stages, so blocks blk+1 and blk+2's K/V loads
-        // (64 KB per workgroup) are in flight while block blk is computed from
-        // LDS; the stage just stored is refilled with block blk+2 at once.
-        // Loads past the segment repeat its last block (same loads on every
-        // path, no use).
-        // (A 64-thread workgroup, G = 1, holds a whole block per thread: one
-        // stage.)
-        constexpr int kAhead = G >= 2 ? 2 : 1;
-        Stage<NT> stg[kAhead];
-        const int blk0 = p - ub;
-        const int blk1 = seg_end - ub;
-        const int blast = blk1 - 1;
-        stage_load<NT>(stg[0], a, block_pages(trow, blk0, ctx), h, blk0 * kMqKeys, ctx);
-        if constexpr (kAhead == 2)
-            stage_load<NT>(stg[1], a, block_pages(trow, min(blk0 + 1, blast), ctx), h,
-                           min(blk0 + 1, blast) * kMqKeys, ctx);
-        // Block blk0 to tile 0 now; its stage then fetches block blk0+kAhead.
-        // (The previous segment ended on a barrier after its last reads.)
-        stage_store<NT>(stg[0], k_lds2[0], vt_lds2[0]);
-        stage_load<NT>(stg[0], a, block_pages(trow, min(blk0 + kAhead, blast), ctx), h,
-                       min(blk0 + kAhead, blast) * kMqKeys, ctx);
-        BlockPages nxt = block_pages(trow, min(blk0 + kAhead + 1, blast), ctx);
-        __syncthreads();
-        // One block: `cur` holds block blk+1; it goes to the other tile and
-        // then fetches block blk+1+kAhead, while block blk is computed.
-        auto do_block = [&](Stage<NT> &cur, int blk) {
-            if (blk + 1 < blk1) {
-                stage_store<NT>(cur, k_lds2[(blk + 1 - blk0) & 1], vt_lds2[(blk + 1 - blk0) & 1]);
-                stage_load<NT>(cur, a, nxt, h, min(blk + 1 + kAhead, blast) * kMqKeys, ctx);
-                nxt = block_pages(trow, min(blk + 2 + kAhead, blast), ctx);
-            }
-            const uint16_t *k_lds = k_lds2[(blk - blk0) & 1];  // block blk0 went to tile 0
-            const uint16_t *vt_lds = vt_lds2[(blk - blk0) & 1];
-            const int key0 = blk * kMqKeys;
-
-            // S^T for keys key0 + 16*nt + 4*grp + i, query column `col`.
-            float4_t s[2];
+            // S^T for keys key0 + 16*nt + 4*grp + i, row `col` of each tile.
+            float4_t s[NT][2];
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
-                s[nt] = float4_t{0.f, 0.f, 0.f, 0.f};
-                const uint16_t *kr = k_lds + (16 * nt + col) * kKRow + 8 * grp;
 #pragma unroll
-                for (int kk = 0; kk < 8; ++kk)
-                    s[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        as_h8(*reinterpret_cast<const uint4 *>(kr + 32 * kk)), as_h8(qb[kk]), s[nt], 0, 0, 0);
-            }
-            float mx = -INFINITY;
+                for (int t = 0; t < NT; ++t) s[t][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+                const uint8_t *kr = kt + (16 * nt + col) * kRowBytes;
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
+                for (int kk = 0; kk < 8; ++kk) {
+                    const uint4 ka = *reinterpret_cast<const uint4 *>(kr + 16 * k_granule(col, 4 * kk + grp));
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int key = key0 + 16 * nt + 4 * grp + i;
-                    bool vis = qvalid && key < ctx;
-                    if (a.tree)
-                        vis = vis && (key < ns || ((qbits >> (key - ns)) & 1ull));
-                    else
-                        vis = vis && key <= qslot;
-                    const float v = vis ? s[nt][i] * scale : -INFINITY;
-                    s[nt][i] = v;
-                    mx = fmaxf(mx, v);
+                    for (int t = 0; t < NT; ++t)
+                        s[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(ka), as_h8(qb[t][kk]), s[t][nt],
+                                                                        0, 0, 0);
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m, mx);
-            const float mu = (mn == -INFINITY) ? 0.0f : mn;  // rows with nothing visible yet
-            const float corr = __builtin_amdgcn_exp2f(m - mu);
-            uint32_t pk[4];
-            float psum = 0.0f;
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                const uint32_t lo = pack_h2(__builtin_amdgcn_exp2f(s[nt][0] - mu), __builtin_amdgcn_exp2f(s[nt][1] - mu));
-                const uint32_t hi = pack_h2(__builtin_amdgcn_exp2f(s[nt][2] - mu), __builtin_amdgcn_exp2f(s[nt][3] - mu));
-                pk[2 * nt] = lo;
-                pk[2 * nt + 1] = hi;
-                psum += (lo_f(lo) + hi_f(lo)) + (lo_f(hi) + hi_f(hi));
             }
-            l = l * corr + psum;
-            m = mn;
-            const half8_t pb = __builtin_bit_cast(half8_t, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+            half8_t pb[NT];
+            float corr[NT];
+            bool rescale = false;
+            // A block wholly before the step's first new slot is visible to
+            // every row (wave-uniform test); otherwise mask key by key.  Rows
+            // past the unit's tokens are never written, so the open case
+            // needs no mask at all.
+            const bool open = key0 + kMqKeys <= cu.ns;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        float v = s[t][nt][i] * scale;
+                        if (!open) {
+                            const int key = key0 + 16 * nt + 4 * grp + i;
+                            bool vis;
+                            if constexpr (TREE) {
+                                // The cache before the step, then the new rows
+                                // in the node's bit set (bits only for the
+                                // step's nodes, so keys past the sequence drop
+                                // out).  Bitwise, so no lane branches.
+                                const int rel = key - cu.ns;
+                                const bool bit = ((qbits[t] >> (rel & 63)) & 1ull) != 0;
+                                vis = qvalid[t] & ((rel < 0) | ((rel < 64) & bit));
+                            } else {
+                                vis = qvalid[t] & (key <= qslot[t]);  // qslot < ctx
+                            }
+                            v = vis ? v : -INFINITY;
+                        }
+                        s[t][nt][i] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                mx = group4_max(mx);
+                // Move the reference max only on a jump past the slack (or
+                // from -inf, where acc and l are still zero).
+                const bool jump = mx > m[t] + kRescaleSlack;
+                const float mn = jump ? mx : m[t];
+                const float mu = (mn == -INFINITY) ? 0.0f : mn;  // rows with nothing visible yet
+                corr[t] = __builtin_amdgcn_exp2f(m[t] - mu);
+                rescale = rescale || (jump && m[t] != -INFINITY);
+                uint32_t pk[4];
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    pk[2 * nt] = pack_h2(__builtin_amdgcn_exp2f(s[t][nt][0] - mu),
+                                         __builtin_amdgcn_exp2f(s[t][nt][1] - mu));
+                    pk[2 * nt + 1] = pack_h2(__builtin_amdgcn_exp2f(s[t][nt][2] - mu),
+                                             __builtin_amdgcn_exp2f(s[t][nt][3] - mu));
+                }
+                // l sums the fp16 probabilities PV uses.
+                constexpr uint32_t kOnes = 0x3c003c00u;  // fp16 pair (1, 1)
+                float psum = dot2(pk[0], kOnes, 0.0f);
+                psum = dot2(pk[1], kOnes, psum);
+                psum = dot2(pk[2], kOnes, psum);
+                psum = dot2(pk[3], kOnes, psum);
+                l[t] = l[t] * corr[t] + psum;
+                m[t] = mn;
+                pb[t] = __builtin_bit_cast(half8_t, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+            }
+            // Rescale only when some row's reference max moved (wave-uniform).
+            if (__builtin_amdgcn_ballot_w64(rescale)) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int dt = 0; dt < 16; ++dt) acc[t][dt] *= corr[t];
+            }
+            // V^T operand of dim tile dt: ds_read_b64_tr_b16 gives lane c of
+            // a 16-lane group column c of the 4 x 16 block whose row r the
+            // group's lanes 4r..4r+3 address, 8 bytes each: here key
+            // 4*grp + r (then 16 + 4*grp + r), dims 16*dt + 4*(lane%4) ...
+            const int vr = (lane & 15) >> 2;
+            const int vs = lane & 3;
 #pragma unroll
             for (int dt = 0; dt < 16; ++dt) {
-                acc[dt] *= corr;
-                const uint16_t *vr = vt_lds + (16 * dt + col) * kVRow + 4 * grp;
-                const uint2 v0 = *reinterpret_cast<const uint2 *>(vr);
-                const uint2 v1 = *reinterpret_cast<const uint2 *>(vr + 16);
-                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(half8_t, make_uint4(v0.x, v0.y, v1.x, v1.y)), pb, acc[dt], 0, 0, 0);
+                short4_t part[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int key = 16 * hh + 4 * grp + vr;
+                    const int p = 2 * dt + (vs >> 1);
+                    const uint8_t *src = vt + key * kRowBytes + 16 * v_granule(key, p) + 8 * (vs & 1);
+                    part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t *)src);
+                }
+                const uint2 v0 = __builtin_bit_cast(uint2, part[0]);
+                const uint2 v1 = __builtin_bit_cast(uint2, part[1]);
+                const half8_t va = __builtin_bit_cast(half8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    acc[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t], acc[t][dt], 0, 0, 0);
             }
-            __syncthreads();  // every wave is done with this tile and the next one is stored
-        };
-        for (int blk = blk0; blk < blk1; blk += 2) {
-            do_block(stg[kAhead - 1], blk);
-            if (blk + 1 >= blk1) break;
-            do_block(stg[0], blk + 1);
+            ++n_done;
         }
 
-        // The four lane groups hold disjoint keys of each query column.
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        const bool whole = p == ub && seg_end == ue;
-        if (whole) {
-            if (qvalid) {
-                const float inv = 1.0f / l;
-                uint16_t *orow = a.out + (static_cast<size_t>(tok_base + qi) * nh + h * G + wave) * kHeadDim;
+        // The four lane groups hold disjoint keys of each row.
 #pragma unroll
-                for (int dt = 0; dt < 16; ++dt) {
-                    uint2 o;
-                    o.x = pack_h2(acc[dt][0] * inv, acc[dt][1] * inv);
-                    o.y = pack_h2(acc[dt][2] * inv, acc[dt][3] * inv);
-                    *reinterpret_cast<uint2 *>(orow + 16 * dt + 4 * grp) = o;
+        for (int t = 0; t < NT; ++t) {
+            const float lt = group4_sum(l[t]);
+            const int rho = 16 * (wv * NT + t) + col;
+            if (whole) {
+                if (qvalid[t]) {
+                    const float inv = 1.0f / lt;
+                    uint16_t *orow =
+                        a.out + (static_cast<size_t>(cu.tok + cu.tile * Q + iq[t]) * nh + cu.h * G + gq[t]) * kHeadDim;
+#pragma unroll
+                    for (int dt = 0; dt < 16; ++dt) {
+                        uint2 o;
+                        o.x = pack_h2(acc[t][dt][0] * inv, acc[t][dt][1] * inv);
+                        o.y = pack_h2(acc[t][dt][2] * inv, acc[t][dt][3] * inv);
+                        *reinterpret_cast<uint2 *>(orow + 16 * dt + 4 * grp) = o;
+                    }
+                }
+            } else {
+                const int slot = 2 * w + (first_seg ? 0 : 1);
+                const size_t rowi = static_cast<size_t>(slot) * kMqSlotRows + rho;
+                float *ar = a.ws_acc + rowi * kHeadDim;
+#pragma unroll
+                for (int dt = 0; dt < 16; ++dt)
+                    *reinterpret_cast<float4 *>(ar + 16 * dt + 4 * grp) =
+                        make_float4(acc[t][dt][0], acc[t][dt][1], acc[t][dt][2], acc[t][dt][3]);
+                if (grp == 0) {
+                    a.ws_ml[rowi * 2] = m[t];
+                    a.ws_ml[rowi * 2 + 1] = lt;
                 }
             }
-        } else {
-            const int slot = 2 * w + (first_seg ? 0 : 1);
-            const size_t rowi = (static_cast<size_t>(slot) * G + wave) * kMqRows + col;
-            float *ar = a.ws_acc + rowi * kHeadDim;
-#pragma unroll
-            for (int dt = 0; dt < 16; ++dt)
-                *reinterpret_cast<float4 *>(ar + 16 * dt + 4 * grp) =
-                    make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
-            if (grp == 0) {
-                a.ws_ml[rowi * 2] = m;
-                a.ws_ml[rowi * 2 + 1] = l;
-            }
         }
-        p = seg_end;
         first_seg = false;
+        if (g >= q1) break;
+        cu = load_unit(a, cu.u + 1, cu.b);
     }
+    // Loads past the share write LDS too: none may land after the
+    // workgroup's LDS is handed on.
+    __builtin_amdgcn_s_waitcnt(0);
 }
 
 // Merge the partials of units cut across workgroups: one workgroup per
-// (unit, head of the group); thread = (query row, 16-dim slice).
-template <int G>
+// (unit, 16 rows of the tile); thread = (row, 16-dim slice).
 __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int u = blockIdx.x;
-    const int wave = blockIdx.y;
     const int ub = a.mq_pre[u];
     const int ue = a.mq_pre[u + 1];
     if (ue == ub) return;
@@ -365,19 +465,23 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int w1 = mq_wg_of(ue - 1, NB, W);
     if (w0 == w1) return;  // written whole by one workgroup
     const int hkv = a.num_kv_heads;
+    const int G = a.num_heads / hkv;
+    const int Q = a.q_tile;
     const int b = upper_index(a.upre, a.n_seqs, u);
     const int x = u - a.upre[b];
     const int tile = x / hkv;
     const int h = x - tile * hkv;
-    const int row = threadIdx.x >> 4;
+    const int rho = 16 * blockIdx.y + (threadIdx.x >> 4);
     const int d0 = (threadIdx.x & 15) * 16;
+    const int iq = rho / G;
+    const int gq = rho - iq * G;
     const int T = a.tok_off[b + 1] - a.tok_off[b];
-    const int qi = tile * kMqRows + row;
-    if (qi >= T) return;
+    const int qi = tile * Q + iq;
+    if (iq >= Q || qi >= T) return;
     float big = -INFINITY;
     for (int ww = w0; ww <= w1; ++ww) {
         const int slot = 2 * ww + (ub <= mq_wg_start(ww, NB, W) ? 0 : 1);
-        big = fmaxf(big, a.ws_ml[((static_cast<size_t>(slot) * G + wave) * kMqRows + row) * 2]);
+        big = fmaxf(big, a.ws_ml[(static_cast<size_t>(slot) * kMqSlotRows + rho) * 2]);
     }
     const float mu = (big == -INFINITY) ? 0.0f : big;
     float lt = 0.0f;
@@ -386,7 +490,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     for (int e = 0; e < 16; ++e) o[e] = 0.0f;
     for (int ww = w0; ww <= w1; ++ww) {
         const int slot = 2 * ww + (ub <= mq_wg_start(ww, NB, W) ? 0 : 1);
-        const size_t rowi = (static_cast<size_t>(slot) * G + wave) * kMqRows + row;
+        const size_t rowi = static_cast<size_t>(slot) * kMqSlotRows + rho;
         const float c = __builtin_amdgcn_exp2f(a.ws_ml[rowi * 2] - mu);
         lt += c * a.ws_ml[rowi * 2 + 1];
         const float4 *src = reinterpret_cast<const float4 *>(a.ws_acc + rowi * kHeadDim + d0);
@@ -400,7 +504,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
         }
     }
     const float inv = 1.0f / lt;
-    uint16_t *orow = a.out + (static_cast<size_t>(a.tok_off[b] + qi) * a.num_heads + h * G + wave) * kHeadDim + d0;
+    uint16_t *orow = a.out + (static_cast<size_t>(a.tok_off[b] + qi) * a.num_heads + h * G + gq) * kHeadDim + d0;
     uint4 o0, o1;
     o0.x = pack_h2(o[0] * inv, o[1] * inv);
     o0.y = pack_h2(o[2] * inv, o[3] * inv);
@@ -414,12 +518,15 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     *reinterpret_cast<uint4 *>(orow + 8) = o1;
 }
 
-template <int G>
-hipError_t launch_mq_g(const MultiQueryArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(mq_kernel<G>, dim3(a.n_wg), dim3(64 * G), 0, s, a);
+template <int NT>
+hipError_t launch_mq_nt(const MultiQueryArgs &a, hipStream_t s) {
+    if (a.tree)
+        hipLaunchKernelGGL((mq_kernel<NT, true>), dim3(a.n_wg), dim3(64 * kWaves), 0, s, a);
+    else
+        hipLaunchKernelGGL((mq_kernel<NT, false>), dim3(a.n_wg), dim3(64 * kWaves), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(mq_combine_kernel<G>, dim3(a.n_units, G), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(mq_combine_kernel, dim3(a.n_units, kWaves * NT), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -427,13 +534,12 @@ hipError_t launch_mq_g(const MultiQueryArgs &a, hipStream_t s) {
 
 hipError_t launch_multi_query(const MultiQueryArgs &a, hipStream_t s) {
     if (a.n_units <= 0 || a.total_blocks <= 0) return hipSuccess;
-    switch (a.num_heads / a.num_kv_heads) {
-        case 1: return launch_mq_g<1>(a, s);
-        case 2: return launch_mq_g<2>(a, s);
-        case 3: return launch_mq_g<3>(a, s);
-        case 4: return launch_mq_g<4>(a, s);
-        case 6: return launch_mq_g<6>(a, s);
-        case 8: return launch_mq_g<8>(a, s);
+    const int G = a.num_heads / a.num_kv_heads;
+    if (G < 1 || G > kMqMaxGroup || a.num_heads % a.num_kv_heads) return hipErrorInvalidValue;
+    if (a.q_tile != mq_tile_tokens(G, a.n_t)) return hipErrorInvalidValue;
+    switch (a.n_t) {
+        case 1: return launch_mq_nt<1>(a, s);
+        case 2: return launch_mq_nt<2>(a, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -51,7 +51,6 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 constexpr int kStageSlots = 4;
 constexpr int kDecodeWgPerCu = 1;   // stream-K decode workgroups per CU
 constexpr int kMinPagesPerWg = 1;   // a short sequence still spreads over several CUs
-constexpr int kMaxGroup = 8;        // largest GQA group the kernels take
 
 }  // namespace
 
@@ -99,8 +98,10 @@ struct kva_cache {
     bool step_valid = false;
     int32_t st_n_seqs = 0, st_n_tok = 0, st_max_ctx = 0, st_max_new = 0, st_max_pos = 0;
     int32_t st_total_pages = 0;  // pages of all sequences of the step
-    int32_t st_mq_units = 0;     // (sequence, 16-token tile, kv head) units
+    int32_t st_mq_units = 0;     // (sequence, token tile, kv head) units
     int32_t st_mq_blocks = 0;    // 32-key blocks of all multi-query units
+    int32_t st_mq_nt = 1;        // 16-row tiles per wave of the multi-query kernel
+    int32_t st_mq_q = 0;         // new tokens per unit tile
     size_t off_upre = 0, off_mqpre = 0;
     bool st_all_one = false, st_has_bits = false;
     size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
@@ -323,9 +324,11 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
     c->free_list.resize(cfg->max_blocks);
     for (int32_t i = 0; i < cfg->max_blocks; ++i) c->free_list[i] = cfg->max_blocks - 1 - i;
     // Step plan: 5 per-sequence arrays + 3 per-token arrays + bits.
-    // Multi-query units: at most (tokens/16 + sequences) tiles per kv head.
+    // Multi-query units: at most (tokens/Q + sequences) tiles per kv head,
+    // Q >= the one-tile token count of the group.
+    const size_t q_min = static_cast<size_t>(kva::mq_tile_tokens(cfg->num_heads / cfg->num_kv_heads, 1));
     const size_t max_units =
-        (static_cast<size_t>(cfg->max_step_tokens) / kva::kMqRows + cfg->max_seqs) * cfg->num_kv_heads;
+        (static_cast<size_t>(cfg->max_step_tokens) / q_min + cfg->max_seqs) * cfg->num_kv_heads;
     c->step_bytes = round_up(sizeof(int32_t) * (6 * static_cast<size_t>(cfg->max_seqs) + 3), 256) +
                     round_up(sizeof(int32_t) * (max_units + 1), 256) +
                     round_up(sizeof(int32_t) * 3 * static_cast<size_t>(cfg->max_step_tokens), 256) +
@@ -369,7 +372,7 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
             return cleanup(hip_fail(e, "hipMalloc(workspace ml)"));
         // Multi-query partial slots: two per workgroup, one workgroup per CU.
         c->mq_max_wg = c->n_cu;
-        const size_t mq_rows = static_cast<size_t>(2) * c->mq_max_wg * kMaxGroup * kva::kMqRows;
+        const size_t mq_rows = static_cast<size_t>(2) * c->mq_max_wg * kva::kMqSlotRows;
         if ((e = hipMalloc(&c->d_mq_acc, mq_rows * kva::kHeadDim * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(multi-query workspace)"));
         if ((e = hipMalloc(&c->d_mq_ml, mq_rows * 2 * sizeof(float))) != hipSuccess)
@@ -614,9 +617,15 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     const size_t o_start = o_ctx + sizeof(int32_t) * n_seqs;
     const size_t o_tokoff = o_start + sizeof(int32_t) * n_seqs;
     const size_t o_pre = o_tokoff + sizeof(int32_t) * (n_seqs + 1);
+    // Multi-query tiling: Q new tokens per unit tile (see mq_tiles_for).
+    const int32_t group = c->cfg.num_heads / c->cfg.num_kv_heads;
+    int32_t run_max = 0;
+    for (int32_t b = 0; b < n_seqs; ++b) run_max = std::max(run_max, n_new[b]);
+    const int32_t mq_nt = kva::mq_tiles_for(group, run_max);
+    const int32_t mq_q = kva::mq_tile_tokens(group, mq_nt);
     int64_t n_units = 0;
     for (int32_t b = 0; b < n_seqs; ++b)
-        n_units += static_cast<int64_t>((n_new[b] + kva::kMqRows - 1) / kva::kMqRows) * c->cfg.num_kv_heads;
+        n_units += static_cast<int64_t>((n_new[b] + mq_q - 1) / mq_q) * c->cfg.num_kv_heads;
     const size_t o_upre = o_pre + sizeof(int32_t) * (n_seqs + 1);
     const size_t o_mqpre = o_upre + sizeof(int32_t) * (n_seqs + 1);
     const size_t o_tseq = round_up(o_mqpre + sizeof(int32_t) * (n_units + 1), 16);
@@ -672,10 +681,9 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     int64_t units = 0, blocks = 0;
     for (int32_t b = 0; b < n_seqs; ++b) {
         p_upre[b] = static_cast<int32_t>(units);
-        const int32_t tiles = (n_new[b] + kva::kMqRows - 1) / kva::kMqRows;
+        const int32_t tiles = (n_new[b] + mq_q - 1) / mq_q;
         for (int32_t tl = 0; tl < tiles; ++tl) {
-            const int64_t keys = tree_bits ? p_ctx[b]
-                                           : p_start[b] + std::min(n_new[b], (tl + 1) * kva::kMqRows);
+            const int64_t keys = tree_bits ? p_ctx[b] : p_start[b] + std::min(n_new[b], (tl + 1) * mq_q);
             const int64_t nb = (keys + kva::kMqKeys - 1) / kva::kMqKeys;
             for (int32_t hh = 0; hh < c->cfg.num_kv_heads; ++hh) {
                 p_mqpre[units++] = static_cast<int32_t>(blocks);
@@ -713,6 +721,8 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->st_total_pages = static_cast<int32_t>(pages);
     c->st_mq_units = static_cast<int32_t>(units);
     c->st_mq_blocks = static_cast<int32_t>(blocks);
+    c->st_mq_nt = mq_nt;
+    c->st_mq_q = mq_q;
     c->off_upre = o_upre;
     c->off_mqpre = o_mqpre;
     c->st_all_one = all_one;
@@ -901,6 +911,8 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
     a.tree = tree ? 1 : 0;
+    a.n_t = c->st_mq_nt;
+    a.q_tile = c->st_mq_q;
     a.ws_acc = c->d_mq_acc;
     a.ws_ml = c->d_mq_ml;
     const hipError_t e = kva::launch_multi_query(a, static_cast<hipStream_t>(stream));

@@ -133,11 +133,21 @@ struct MultiQueryArgs {
     int32_t num_heads;
     int32_t num_kv_heads;
     int32_t tree;             // 0 = causal chunk, 1 = tree mask
-    float *ws_acc;            // [2*n_wg][G][16][256] partial slots
-    float *ws_ml;             // [2*n_wg][G][16][2]
+    int32_t n_t;              // 16-row MFMA tiles per wave (1 or 2)
+    int32_t q_tile;           // new tokens per unit tile: mq_tile_tokens(G, n_t)
+    float *ws_acc;            // [2*n_wg][kMqSlotRows][256] partial slots
+    float *ws_ml;             // [2*n_wg][kMqSlotRows][2]
 };
-constexpr int kMqKeys = 32;   // keys per multi-query block
-constexpr int kMqRows = 16;   // query tokens per unit tile
+constexpr int kMqKeys = 32;       // keys per multi-query block
+constexpr int kMqMaxGroup = 8;    // largest GQA group of the multi-query kernel
+constexpr int kMqMaxTiles = 2;    // largest n_t
+constexpr int kMqSlotRows = 4 * 16 * kMqMaxTiles;  // query rows of a partial slot
+// A unit's query rows are (token, head) pairs of the GQA group, 64 per
+// 16-row tile of its four waves: tokens per unit tile.
+constexpr int mq_tile_tokens(int G, int n_t) { return 64 * n_t / G; }
+// Tiles per wave for a step whose longest new-token run is max_new: one
+// when a whole run fits one unit, else two.
+constexpr int mq_tiles_for(int G, int max_new) { return max_new * G <= 64 ? 1 : 2; }
 hipError_t launch_multi_query(const MultiQueryArgs &a, hipStream_t s);
 
 }  // namespace kva

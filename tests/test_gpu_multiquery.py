@@ -125,6 +125,21 @@ def test_prefill_c4_workload(device):
     cache.destroy()
 
 
+@pytest.mark.parametrize("heads,kv", [(8, 8), (12, 4), (16, 2), (8, 2)])
+def test_multi_query_groups(device, heads, kv):
+    """GQA groups 1, 3, 8 and 4: a unit's query rows pack (token, head)
+    pairs, so the tile's token count and row layout depend on the group.
+    Causal chunks long enough for two tiles per wave, and a 9-node tree
+    (one tile per wave, except for a group of 8)."""
+    say(f"multi-query groups heads={heads} kv={kv}")
+    got, exp = run_prefilled(device, [37, 0, 130], [70, 9, 140], num_heads=heads, num_kv_heads=kv,
+                             seed=heads * 10 + kv)
+    assert max_err(got, exp) <= TOL
+    got, exp = run_prefilled(device, [300, 20, 1], [9, 9, 9], num_heads=heads, num_kv_heads=kv,
+                             seed=heads * 10 + kv + 1, tree_parents=C5_PARENTS)
+    assert max_err(got, exp) <= TOL
+
+
 def test_tree_verify_small(device):
     say("tree verify small")
     got, exp = run_prefilled(device, [100, 37, 2000, 0], [9, 9, 9, 9], seed=5, tree_parents=C5_PARENTS)
