@@ -85,6 +85,79 @@ __device__ __forceinline__ int32_t ld_uniform(const int32_t *p) {
         reinterpret_cast<uintptr_t>(p));
 }
 
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
+
+// LDS byte address of a __shared__ location.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t *)p));
+}
+
+// One 16-byte-per-lane buffer load written straight to LDS: lane l's bytes
+// go to lds + 16*l.  Written as inline assembly on purpose: the compiler
+// would otherwise order every later LDS read of the kernel behind all such
+// loads in flight (it cannot tell a ring's stages apart), which would drain
+// the ring at every step.  Kernels do their own waiting (wait_vm + a
+// barrier); to the compiler these loads are invisible, so its own load
+// waits can only grow stricter, never too weak.
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(lds), "v"(voff), "s"(r)
+        : "memory", "m0");
+}
+
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding (they complete in order).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    // s_waitcnt fields: vmcnt[3:0], expcnt[6:4] (7 = no wait), lgkmcnt[11:8]
+    // (15 = no wait), vmcnt[5:4] in bits [15:14].
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Read-only buffer resource over [base, base + bytes); bytes = 0 makes every
+// access out of range (loads fetch nothing, and still count).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ro_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+
+// Max / sum over the four 16-lane groups (every lane gets it): permlane
+// swaps, VALU only (no LDS round trip).  v_permlane16_swap with both
+// operands holding x leaves x of rows 0,0,2,2 in the first and of rows
+// 1,1,3,3 in the second register; v_permlane32_swap likewise pairs the
+// halves, so combining the two registers after each covers all four.
+// Inline assembly: with one value in both operands the compiler's builtin
+// has been seen to read the first result twice.
+__device__ __forceinline__ void swap16(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap32(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float group4_max(float x) {
+    float a = x, b = x;
+    swap16(a, b);
+    a = fmaxf(a, b);
+    b = a;
+    swap32(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float group4_sum(float x) {
+    float a = x, b = x;
+    swap16(a, b);
+    a += b;
+    b = a;
+    swap32(a, b);
+    return a + b;
+}
+
 __device__ __forceinline__ uint4 ld16(const uint16_t *p) {
     return *reinterpret_cast<const uint4 *>(p);
 }

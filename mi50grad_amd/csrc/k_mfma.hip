@@ -51,9 +51,6 @@ constexpr int kRowBytes = kHeadDim * 2;             // 512 B: one key of one hea
 constexpr int kDmaPerWave = 8;                      // 4 K + 4 V loads per block
 constexpr float kLog2e = 1.4426950408889634f;
 
-typedef short short4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 __device__ __forceinline__ int mq_wg_start(int w, int n, int W) {
     return static_cast<int>(static_cast<int64_t>(w) * n / W);
@@ -110,28 +107,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t pool_rsrc(const uint16_t *base
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
 }
 
-// LDS byte address of a __shared__ location.
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t *)p));
-}
-
-// One 16-byte-per-lane buffer load written straight to LDS: lane l's bytes
-// go to lds + 16*l.  Written as inline assembly on purpose: the compiler
-// would otherwise order every later LDS read of the kernel behind all such
-// loads in flight (it cannot tell the ring's stages apart), which would
-// drain the ring at every block.  The kernel does its own waiting
-// (wait_block + barrier); to the compiler these loads are invisible, so its
-// own load waits can only grow stricter, never too weak.
-__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t voff) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %1, %2, 0 offen lds"
-        :
-        : "s"(lds), "v"(voff), "s"(r)
-        : "memory", "m0");
-}
-
 // Issue this wave's share of block g of unit un into LDS stage `st`: keys
 // 8*wv..8*wv+7 of the block (one page), K and V, four 1 KB loads each (lane
 // l writes granule l%32 of key 2i + l/32).  Keys past the sequence read its
@@ -157,47 +132,11 @@ __device__ __forceinline__ void issue_block(uint8_t *st, const MultiQueryArgs &a
     }
 }
 
-// Wait until at most kDmaPerWave * (kRing - 2) of this wave's loads are
-// outstanding (loads complete in order): block i's have landed in LDS while
-// blocks i+1 and i+2 may still be in flight.
-__device__ __forceinline__ void wait_block() {
-    constexpr int n = kDmaPerWave * (kRing - 2);
-    // s_waitcnt fields: vmcnt[3:0], expcnt[6:4] (7 = no wait), lgkmcnt[11:8]
-    // (15 = no wait), vmcnt[5:4] in bits [15:14].
-    __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14));
-}
+// Block i's loads have landed in LDS when at most the loads of blocks i+1
+// and i+2 are outstanding.
+__device__ __forceinline__ void wait_block() { wait_vm<kDmaPerWave * (kRing - 2)>(); }
 
 __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
-
-// Max / sum over the four 16-lane groups (every lane gets it): permlane
-// swaps, VALU only (no LDS round trip).  v_permlane16_swap with both
-// operands holding x leaves x of rows 0,0,2,2 in the first and of rows
-// 1,1,3,3 in the second register; v_permlane32_swap likewise pairs the
-// halves, so combining the two registers after each covers all four.
-// Inline assembly: with one value in both operands the compiler's builtin
-// has been seen to read the first result twice.
-__device__ __forceinline__ void swap16(float &a, float &b) {
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ void swap32(float &a, float &b) {
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-}
-__device__ __forceinline__ float group4_max(float x) {
-    float a = x, b = x;
-    swap16(a, b);
-    a = fmaxf(a, b);
-    b = a;
-    swap32(a, b);
-    return fmaxf(a, b);
-}
-__device__ __forceinline__ float group4_sum(float x) {
-    float a = x, b = x;
-    swap16(a, b);
-    a += b;
-    b = a;
-    swap32(a, b);
-    return a + b;
-}
 
 // A row's reference max moves only when a block's max exceeds it by more
 // than this (log2 units): probabilities then stay below 2^8 (fp16 holds
