@@ -44,11 +44,9 @@
 namespace kva {
 namespace {
 
-constexpr int kWaves = 4;
 constexpr int kRing = 4;                            // LDS stages
 constexpr int kTileBytes = kMqKeys * kHeadDim * 2;  // 16 KB: K or V of a block
 constexpr int kRowBytes = kHeadDim * 2;             // 512 B: one key of one head
-constexpr int kDmaPerWave = 8;                      // 4 K + 4 V loads per block
 constexpr float kLog2e = 1.4426950408889634f;
 
 
@@ -88,7 +86,7 @@ struct Unit {
 __device__ __forceinline__ Unit load_unit(const MultiQueryArgs &a, int u, int b) {
     Unit x;
     x.u = u;
-    x.ub = ld_uniform(a.mq_pre + u);
+    x.ub = ld_uniform(a.mq_pre + u) + kMqUnitCost;  // its first block (positions before: the start cost)
     x.ue = ld_uniform(a.mq_pre + u + 1);
     while (ld_uniform(a.upre + b + 1) <= u) ++b;  // units are in sequence order
     x.b = b;
@@ -108,33 +106,37 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t pool_rsrc(const uint16_t *base
 }
 
 // Issue this wave's share of block g of unit un into LDS stage `st`: keys
-// 8*wv..8*wv+7 of the block (one page), K and V, four 1 KB loads each (lane
-// l writes granule l%32 of key 2i + l/32).  Keys past the sequence read its
-// last key (finite data; the mask drops them).  A disabled issue (past the
-// workgroup's share) goes through an empty resource: no memory access, but
-// the same loads, so every wave's load counter advances alike.
+// kPer*wv .. kPer*wv + kPer-1 of the block (kPer = 32/WAVES, within one
+// page), K and V, one 1 KB load per two keys each (lane l writes granule
+// l%32 of key 2i + l/32).  Keys past the sequence read its last key (finite
+// data; the mask drops them).  A disabled issue (past the workgroup's share)
+// goes through an empty resource: no memory access, but the same loads, so
+// every wave's load counter advances alike.
+template <int WAVES>
 __device__ __forceinline__ void issue_block(uint8_t *st, const MultiQueryArgs &a, const Unit &un, int g, bool on,
                                             int wv, int lane, int row_bytes) {
-    const int key0 = (g - un.ub) * kMqKeys + 8 * wv;  // key of the unit
+    constexpr int kPer = kMqKeys / WAVES;
+    const int key0 = (g - un.ub) * kMqKeys + kPer * wv;  // key of the unit
     const int last = un.ctx - 1;
     const int page = on ? ld_uniform(un.trow + (min(key0, last) >> 4)) : 0;
     const size_t off = (static_cast<size_t>(page) * kBlockTokens * row_bytes + un.h * kRowBytes) / 2;
     const uint32_t n = on ? kBlockTokens * row_bytes : 0u;
-    const auto rk = pool_rsrc(a.k_pool + off, n), rv = pool_rsrc(a.v_pool + off, n);
+    const auto rk = ro_rsrc(a.k_pool + off, n), rv = ro_rsrc(a.v_pool + off, n);
     const int q = lane & 31;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int kl = 8 * wv + 2 * i + (lane >> 5);  // key within the block
+    for (int i = 0; i < kPer / 2; ++i) {
+        const int kl = kPer * wv + 2 * i + (lane >> 5);  // key within the block
         const int row = min(key0 + 2 * i + (lane >> 5), last) & 15;
-        const uint32_t dst = lds_addr(st + (8 * wv + 2 * i) * kRowBytes);  // keys 8wv+2i, +1: this load's 1 KB
+        const uint32_t dst = lds_addr(st + (kPer * wv + 2 * i) * kRowBytes);  // this load's 1 KB
         load_to_lds(rk, dst, row * row_bytes + 16 * k_granule(kl, q));
         load_to_lds(rv, dst + kTileBytes, row * row_bytes + 16 * v_granule(kl, q));
     }
 }
 
 // Block i's loads have landed in LDS when at most the loads of blocks i+1
-// and i+2 are outstanding.
-__device__ __forceinline__ void wait_block() { wait_vm<kDmaPerWave * (kRing - 2)>(); }
+// and i+2 (kMqKeys/WAVES loads each per wave) are outstanding.
+template <int WAVES>
+__device__ __forceinline__ void wait_block() { wait_vm<kMqKeys / WAVES * (kRing - 2)>(); }
 
 __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
@@ -144,8 +146,8 @@ __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(ha
 // only on such jumps, not at every block where some row's max grew.
 constexpr float kRescaleSlack = 8.0f;
 
-template <int NT, bool TREE>
-__global__ __launch_bounds__(64 * kWaves) void mq_kernel(MultiQueryArgs a) {
+template <int NT, int WAVES, bool TREE>
+__global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[kRing][2 * kTileBytes];
     const int w = blockIdx.x;
     const int W = a.n_wg;
@@ -177,19 +179,22 @@ __global__ __launch_bounds__(64 * kWaves) void mq_kernel(MultiQueryArgs a) {
     // of the compute side, across unit boundaries.
     const int u0 = upper_index(a.mq_pre, a.n_units, q0);
     Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0));
-    int ig = q0;
+    int ig = max(q0, iu.ub);
+    if (ig >= q1) return;  // the share holds only a unit's start cost
     auto issue = [&](int slot) {
         const bool on = ig < q1;
-        issue_block(ring[slot], a, iu, ig, on, wv, lane, row_bytes);
-        if (on && ++ig < q1 && ig >= iu.ue) iu = load_unit(a, iu.u + 1, iu.b);
+        issue_block<WAVES>(ring[slot], a, iu, ig, on, wv, lane, row_bytes);
+        if (on && ++ig < q1 && ig >= iu.ue) {
+            iu = load_unit(a, iu.u + 1, iu.b);
+            ig = iu.ub;
+        }
     };
     Unit cu = iu;
+    int g = ig;
 #pragma unroll
     for (int s = 0; s + 1 < kRing; ++s) issue(s);
 
     int n_done = 0;  // blocks computed by this workgroup (ring position)
-    int g = q0;
-    bool first_seg = true;
     while (true) {
         const int seg_end = min(cu.ue, q1);
         const bool whole = g == cu.ub && seg_end == cu.ue;
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(64 * kWaves) void mq_kernel(MultiQueryArgs a) {
         }
 
         for (; g < seg_end; ++g) {
-            wait_block();
+            wait_block<WAVES>();
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
             issue((n_done + kRing - 1) % kRing);
@@ -369,7 +374,9 @@ __global__ __launch_bounds__(64 * kWaves) void mq_kernel(MultiQueryArgs a) {
                     }
                 }
             } else {
-                const int slot = 2 * w + (first_seg ? 0 : 1);
+                // Slot 2w: the unit began at or before this share (its first
+                // segment); slot 2w+1: the share's last segment.
+                const int slot = 2 * w + (cu.ub <= q0 ? 0 : 1);
                 const size_t rowi = static_cast<size_t>(slot) * kMqSlotRows + rho;
                 float *ar = a.ws_acc + rowi * kHeadDim;
 #pragma unroll
@@ -382,9 +389,10 @@ __global__ __launch_bounds__(64 * kWaves) void mq_kernel(MultiQueryArgs a) {
                 }
             }
         }
-        first_seg = false;
         if (g >= q1) break;
         cu = load_unit(a, cu.u + 1, cu.b);
+        g = cu.ub;
+        if (g >= q1) break;  // the share ends inside the next unit's start cost
     }
     // Loads past the share write LDS too: none may land after the
     // workgroup's LDS is handed on.
@@ -395,9 +403,9 @@ __global__ __launch_bounds__(64 * kWaves) void mq_kernel(MultiQueryArgs a) {
 // (unit, 16 rows of the tile); thread = (row, 16-dim slice).
 __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int u = blockIdx.x;
-    const int ub = a.mq_pre[u];
+    const int ub = a.mq_pre[u] + kMqUnitCost;  // the unit's first block
     const int ue = a.mq_pre[u + 1];
-    if (ue == ub) return;
+    if (ue <= ub) return;
     const int W = a.n_wg;
     const int NB = a.total_blocks;
     const int w0 = mq_wg_of(ub, NB, W);
@@ -457,15 +465,15 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     *reinterpret_cast<uint4 *>(orow + 8) = o1;
 }
 
-template <int NT>
-hipError_t launch_mq_nt(const MultiQueryArgs &a, hipStream_t s) {
+template <int NT, int WAVES>
+hipError_t launch_mq(const MultiQueryArgs &a, hipStream_t s) {
     if (a.tree)
-        hipLaunchKernelGGL((mq_kernel<NT, true>), dim3(a.n_wg), dim3(64 * kWaves), 0, s, a);
+        hipLaunchKernelGGL((mq_kernel<NT, WAVES, true>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
     else
-        hipLaunchKernelGGL((mq_kernel<NT, false>), dim3(a.n_wg), dim3(64 * kWaves), 0, s, a);
+        hipLaunchKernelGGL((mq_kernel<NT, WAVES, false>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(mq_combine_kernel, dim3(a.n_units, kWaves * NT), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(mq_combine_kernel, dim3(a.n_units, WAVES * NT), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -475,12 +483,11 @@ hipError_t launch_multi_query(const MultiQueryArgs &a, hipStream_t s) {
     if (a.n_units <= 0 || a.total_blocks <= 0) return hipSuccess;
     const int G = a.num_heads / a.num_kv_heads;
     if (G < 1 || G > kMqMaxGroup || a.num_heads % a.num_kv_heads) return hipErrorInvalidValue;
-    if (a.q_tile != mq_tile_tokens(G, a.n_t)) return hipErrorInvalidValue;
-    switch (a.n_t) {
-        case 1: return launch_mq_nt<1>(a, s);
-        case 2: return launch_mq_nt<2>(a, s);
-        default: return hipErrorInvalidValue;
-    }
+    if (a.q_tile != mq_tile_tokens(G, a.n_waves, a.n_t)) return hipErrorInvalidValue;
+    if (a.n_t == 1 && a.n_waves == 4) return launch_mq<1, 4>(a, s);
+    if (a.n_t == 2 && a.n_waves == 4) return launch_mq<2, 4>(a, s);
+    if (a.n_t == 1 && a.n_waves == 8) return launch_mq<1, 8>(a, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace kva

@@ -100,7 +100,7 @@ struct kva_cache {
     int32_t st_total_pages = 0;  // pages of all sequences of the step
     int32_t st_mq_units = 0;     // (sequence, token tile, kv head) units
     int32_t st_mq_blocks = 0;    // 32-key blocks of all multi-query units
-    int32_t st_mq_nt = 1;        // 16-row tiles per wave of the multi-query kernel
+    int32_t st_mq_waves = 4;     // waves per workgroup of the multi-query kernel
     int32_t st_mq_q = 0;         // new tokens per unit tile
     size_t off_upre = 0, off_mqpre = 0;
     bool st_all_one = false, st_has_bits = false;
@@ -326,7 +326,7 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
     // Step plan: 5 per-sequence arrays + 3 per-token arrays + bits.
     // Multi-query units: at most (tokens/Q + sequences) tiles per kv head,
     // Q >= the one-tile token count of the group.
-    const size_t q_min = static_cast<size_t>(kva::mq_tile_tokens(cfg->num_heads / cfg->num_kv_heads, 1));
+    const size_t q_min = static_cast<size_t>(kva::mq_tile_tokens(cfg->num_heads / cfg->num_kv_heads, 4, 1));
     const size_t max_units =
         (static_cast<size_t>(cfg->max_step_tokens) / q_min + cfg->max_seqs) * cfg->num_kv_heads;
     c->step_bytes = round_up(sizeof(int32_t) * (6 * static_cast<size_t>(cfg->max_seqs) + 3), 256) +
@@ -621,8 +621,8 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     const int32_t group = c->cfg.num_heads / c->cfg.num_kv_heads;
     int32_t run_max = 0;
     for (int32_t b = 0; b < n_seqs; ++b) run_max = std::max(run_max, n_new[b]);
-    const int32_t mq_nt = kva::mq_tiles_for(group, run_max);
-    const int32_t mq_q = kva::mq_tile_tokens(group, mq_nt);
+    const int32_t mq_waves = kva::mq_waves_for(group, run_max);
+    const int32_t mq_q = kva::mq_tile_tokens(group, mq_waves, 1);
     int64_t n_units = 0;
     for (int32_t b = 0; b < n_seqs; ++b)
         n_units += static_cast<int64_t>((n_new[b] + mq_q - 1) / mq_q) * c->cfg.num_kv_heads;
@@ -687,7 +687,7 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
             const int64_t nb = (keys + kva::kMqKeys - 1) / kva::kMqKeys;
             for (int32_t hh = 0; hh < c->cfg.num_kv_heads; ++hh) {
                 p_mqpre[units++] = static_cast<int32_t>(blocks);
-                blocks += nb;
+                blocks += kva::kMqUnitCost + nb;
             }
         }
     }
@@ -721,7 +721,7 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->st_total_pages = static_cast<int32_t>(pages);
     c->st_mq_units = static_cast<int32_t>(units);
     c->st_mq_blocks = static_cast<int32_t>(blocks);
-    c->st_mq_nt = mq_nt;
+    c->st_mq_waves = mq_waves;
     c->st_mq_q = mq_q;
     c->off_upre = o_upre;
     c->off_mqpre = o_mqpre;
@@ -911,7 +911,8 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
     a.tree = tree ? 1 : 0;
-    a.n_t = c->st_mq_nt;
+    a.n_waves = c->st_mq_waves;
+    a.n_t = 1;
     a.q_tile = c->st_mq_q;
     a.ws_acc = c->d_mq_acc;
     a.ws_ml = c->d_mq_ml;

@@ -125,29 +125,35 @@ struct MultiQueryArgs {
     const int32_t *tok_off;   // device [n_seqs+1]: new-token ranges
     const uint64_t *tok_bits; // device [T] (tree mode) or null
     const int32_t *upre;      // device [n_seqs+1]: units of earlier sequences
-    const int32_t *mq_pre;    // device [n_units+1]: key blocks of earlier units
+    const int32_t *mq_pre;    // device [n_units+1]: positions of earlier units (blocks + kMqUnitCost each)
     int32_t n_seqs;
     int32_t n_units;          // (sequence, 16-token tile, kv head) units
-    int32_t total_blocks;     // key blocks of all units
+    int32_t total_blocks;     // positions of all units (blocks + kMqUnitCost each)
     int32_t n_wg;             // workgroups sharing the blocks (stream-K)
     int32_t num_heads;
     int32_t num_kv_heads;
     int32_t tree;             // 0 = causal chunk, 1 = tree mask
+    int32_t n_waves;          // waves per workgroup (4 or 8)
     int32_t n_t;              // 16-row MFMA tiles per wave (1 or 2)
-    int32_t q_tile;           // new tokens per unit tile: mq_tile_tokens(G, n_t)
+    int32_t q_tile;           // new tokens per unit tile: mq_tile_tokens(G, n_waves, n_t)
     float *ws_acc;            // [2*n_wg][kMqSlotRows][256] partial slots
     float *ws_ml;             // [2*n_wg][kMqSlotRows][2]
 };
 constexpr int kMqKeys = 32;       // keys per multi-query block
+// The stream-K split of the multi-query kernel counts each unit as this many
+// blocks more than it has (the cost of starting a unit: its query rows,
+// its output), so a share full of short units gets fewer blocks.  Unit u's
+// blocks sit at positions [mq_pre[u] + kMqUnitCost, mq_pre[u+1]).
+constexpr int kMqUnitCost = 2;
 constexpr int kMqMaxGroup = 8;    // largest GQA group of the multi-query kernel
-constexpr int kMqMaxTiles = 2;    // largest n_t
-constexpr int kMqSlotRows = 4 * 16 * kMqMaxTiles;  // query rows of a partial slot
-// A unit's query rows are (token, head) pairs of the GQA group, 64 per
-// 16-row tile of its four waves: tokens per unit tile.
-constexpr int mq_tile_tokens(int G, int n_t) { return 64 * n_t / G; }
-// Tiles per wave for a step whose longest new-token run is max_new: one
-// when a whole run fits one unit, else two.
-constexpr int mq_tiles_for(int G, int max_new) { return max_new * G <= 64 ? 1 : 2; }
+constexpr int kMqSlotRows = 128;  // query rows of a partial slot (waves x 16 x tiles at most)
+// A unit's query rows are (token, head) pairs of the GQA group, 16 per
+// MFMA tile, n_t tiles per wave: tokens per unit tile.
+constexpr int mq_tile_tokens(int G, int n_waves, int n_t) { return 16 * n_waves * n_t / G; }
+// Waves for a step whose longest new-token run is max_new: four (one per
+// SIMD) when a whole run fits one unit of 64 rows (tree verify), else eight
+// (128 rows; two waves per SIMD hide each other's softmax and LDS waits).
+constexpr int mq_waves_for(int G, int max_new) { return max_new * G <= 64 ? 4 : 8; }
 hipError_t launch_multi_query(const MultiQueryArgs &a, hipStream_t s);
 
 }  // namespace kva
