@@ -45,8 +45,9 @@ namespace kva {
 namespace {
 
 constexpr int kRing = 4;                            // LDS stages
-constexpr int kTileBytes = kMqKeys * kHeadDim * 2;  // 16 KB: K or V of a block
 constexpr int kRowBytes = kHeadDim * 2;             // 512 B: one key of one head
+constexpr int kPairBytes = 2 * kRowBytes + 32;      // two keys, then 32 B of padding
+constexpr int kTileBytes = kMqKeys / 2 * kPairBytes;  // K or V of a block (16.5 KB)
 constexpr float kLog2e = 1.4426950408889634f;
 
 
@@ -69,11 +70,16 @@ __device__ __forceinline__ int upper_index(const int32_t *pre, int n, int x) {
     return lo;
 }
 
-// Swizzled 16-byte granule of a 512-byte key row in LDS (key = key index
-// within the block).  K reads take 16 consecutive keys at one granule, V^T
-// reads 4 consecutive keys at two neighbouring granules.
-__device__ __forceinline__ int k_granule(int key, int p) { return p ^ (key & 15); }
-__device__ __forceinline__ int v_granule(int key, int p) { return p ^ ((key & 7) << 1); }
+// LDS layout of a K or V tile: keys in pairs (one 1 KB load each) 1056 B
+// apart, and in odd keys the 16-byte granules swapped in twos (K) or fours
+// (V).  The padding and the swaps spread both read patterns over all banks
+// — K reads take 16 consecutive keys at one granule, V^T reads 4
+// consecutive keys at two neighbouring granules — while every read of a
+// lane stays at a fixed offset from one base, so the addresses are
+// immediates (key = key index within the block).
+__device__ __forceinline__ int key_off(int key) { return (key >> 1) * kPairBytes + (key & 1) * kRowBytes; }
+__device__ __forceinline__ int k_granule(int key, int p) { return p ^ (key & 1); }
+__device__ __forceinline__ int v_granule(int key, int p) { return p ^ ((key & 1) << 2); }
 
 // The facts of one unit (all wave-uniform, read by scalar loads).
 struct Unit {
@@ -101,8 +107,13 @@ __device__ __forceinline__ Unit load_unit(const MultiQueryArgs &a, int u, int b)
     return x;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t pool_rsrc(const uint16_t *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t *>(base), 0, bytes, 0x00020000);
+// Page of this wave's keys of block g of unit un (see issue_block).  (Read
+// a block ahead, at the end of the previous block, it measured 10 % slower
+// on config 4.)
+template <int WAVES>
+__device__ __forceinline__ int block_page(const Unit &un, int g, bool on, int wv) {
+    const int key0 = (g - un.ub) * kMqKeys + kMqKeys / WAVES * wv;
+    return on ? ld_uniform(un.trow + (min(key0, un.ctx - 1) >> 4)) : 0;
 }
 
 // Issue this wave's share of block g of unit un into LDS stage `st`: keys
@@ -114,11 +125,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t pool_rsrc(const uint16_t *base
 // every wave's load counter advances alike.
 template <int WAVES>
 __device__ __forceinline__ void issue_block(uint8_t *st, const MultiQueryArgs &a, const Unit &un, int g, bool on,
-                                            int wv, int lane, int row_bytes) {
+                                            int page, int wv, int lane, int row_bytes) {
     constexpr int kPer = kMqKeys / WAVES;
     const int key0 = (g - un.ub) * kMqKeys + kPer * wv;  // key of the unit
     const int last = un.ctx - 1;
-    const int page = on ? ld_uniform(un.trow + (min(key0, last) >> 4)) : 0;
     const size_t off = (static_cast<size_t>(page) * kBlockTokens * row_bytes + un.h * kRowBytes) / 2;
     const uint32_t n = on ? kBlockTokens * row_bytes : 0u;
     const auto rk = ro_rsrc(a.k_pool + off, n), rv = ro_rsrc(a.v_pool + off, n);
@@ -127,7 +137,7 @@ __device__ __forceinline__ void issue_block(uint8_t *st, const MultiQueryArgs &a
     for (int i = 0; i < kPer / 2; ++i) {
         const int kl = kPer * wv + 2 * i + (lane >> 5);  // key within the block
         const int row = min(key0 + 2 * i + (lane >> 5), last) & 15;
-        const uint32_t dst = lds_addr(st + (kPer * wv + 2 * i) * kRowBytes);  // this load's 1 KB
+        const uint32_t dst = lds_addr(st + (kPer * wv / 2 + i) * kPairBytes);  // this load's two keys
         load_to_lds(rk, dst, row * row_bytes + 16 * k_granule(kl, q));
         load_to_lds(rv, dst + kTileBytes, row * row_bytes + 16 * v_granule(kl, q));
     }
@@ -181,9 +191,11 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
     Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0));
     int ig = max(q0, iu.ub);
     if (ig >= q1) return;  // the share holds only a unit's start cost
+    int ipage = 0;  // page of the next issue
+    auto fetch_page = [&]() { ipage = block_page<WAVES>(iu, ig, ig < q1, wv); };
     auto issue = [&](int slot) {
         const bool on = ig < q1;
-        issue_block<WAVES>(ring[slot], a, iu, ig, on, wv, lane, row_bytes);
+        issue_block<WAVES>(ring[slot], a, iu, ig, on, ipage, wv, lane, row_bytes);
         if (on && ++ig < q1 && ig >= iu.ue) {
             iu = load_unit(a, iu.u + 1, iu.b);
             ig = iu.ub;
@@ -192,7 +204,10 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
     Unit cu = iu;
     int g = ig;
 #pragma unroll
-    for (int s = 0; s + 1 < kRing; ++s) issue(s);
+    for (int s = 0; s + 1 < kRing; ++s) {
+        fetch_page();
+        issue(s);
+    }
 
     int n_done = 0;  // blocks computed by this workgroup (ring position)
     while (true) {
@@ -239,10 +254,11 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             wait_block<WAVES>();
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
+            fetch_page();
             issue((n_done + kRing - 1) % kRing);
             __builtin_amdgcn_sched_barrier(0);
             const uint8_t *kt = ring[n_done % kRing];
-            const uint8_t *vt = kt + kTileBytes;
+            const uint8_t *kbase = kt + key_off(col) + 16 * k_granule(col, grp);
             const int key0 = (g - cu.ub) * kMqKeys;
 
             // S^T for keys key0 + 16*nt + 4*grp + i, row `col` of each tile.
@@ -251,10 +267,11 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) s[t][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
-                const uint8_t *kr = kt + (16 * nt + col) * kRowBytes;
+                // key 16*nt + col, granule 4*kk + grp: kbase + nt*8 pairs + 64*kk
+                const uint8_t *kr = kbase + 8 * nt * kPairBytes;
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) {
-                    const uint4 ka = *reinterpret_cast<const uint4 *>(kr + 16 * k_granule(col, 4 * kk + grp));
+                    const uint4 ka = *reinterpret_cast<const uint4 *>(kr + 64 * kk);
 #pragma unroll
                     for (int t = 0; t < NT; ++t)
                         s[t][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(ka), as_h8(qb[t][kk]), s[t][nt],
@@ -333,16 +350,19 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             // a 16-lane group column c of the 4 x 16 block whose row r the
             // group's lanes 4r..4r+3 address, 8 bytes each: here key
             // 4*grp + r (then 16 + 4*grp + r), dims 16*dt + 4*(lane%4) ...
+            // Key 16*hh + 4*grp + vr, granule 2*dt + vs/2: for odd keys the
+            // swap of fours moves dims 32*dt.. by +-64 B, + when bit 1 of dt
+            // is clear, - when set, so two bases cover every dt.
             const int vr = (lane & 15) >> 2;
             const int vs = lane & 3;
+            const uint8_t *vb = kt + kTileBytes + key_off(4 * grp + vr) + 16 * (vs >> 1) + 8 * (vs & 1);
+            const uint8_t *vbase[2] = {vb + 64 * (vr & 1), vb - 64 * (vr & 1)};
 #pragma unroll
             for (int dt = 0; dt < 16; ++dt) {
                 short4_t part[2];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    const int key = 16 * hh + 4 * grp + vr;
-                    const int p = 2 * dt + (vs >> 1);
-                    const uint8_t *src = vt + key * kRowBytes + 16 * v_granule(key, p) + 8 * (vs & 1);
+                    const uint8_t *src = vbase[(dt >> 1) & 1] + 8 * hh * kPairBytes + 32 * dt;
                     part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t *)src);
                 }
                 const uint2 v0 = __builtin_bit_cast(uint2, part[0]);
