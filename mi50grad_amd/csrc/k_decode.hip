@@ -67,38 +67,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const char *base, ui
 // compiler's load counters stay exact across the branch.
 __device__ __forceinline__ void load_half(HalfPage &p, const char *kb, const char *vb, int lim, bool on,
                                           uint32_t koff, uint32_t voff, int row_bytes) {
-    if (!on || lim >= kBlockTokens) {
-        const uint32_t n = on ? 0x7fffffffu : 0u;
-        const auto rk = page_rsrc(kb, n), rv = page_rsrc(vb, n);
+    const uint32_t n = on ? static_cast<uint32_t>(lim * row_bytes) : 0u;
+    const auto rk = page_rsrc(kb, n), rv = page_rsrc(vb, n);
 #pragma unroll
-        for (int t4 = 0; t4 < 2; ++t4)
+    for (int t4 = 0; t4 < 2; ++t4)
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const auto x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 256 * q, t4 * 4 * row_bytes, 0);
-                p.k[t4][q] = make_uint4(x[0], x[1], x[2], x[3]);
-            }
-#pragma unroll
-        for (int t = 0; t < kHalf; ++t) {
-            const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, t * row_bytes, 0);
-            p.v[t] = make_uint2(x[0], x[1]);
+        for (int q = 0; q < 2; ++q) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + t4 * 4 * row_bytes + 256 * q, 0, 0);
+            p.k[t4][q] = make_uint4(x[0], x[1], x[2], x[3]);
         }
-    } else {
-        const uint32_t n = static_cast<uint32_t>(lim * row_bytes);
-        const auto rk = page_rsrc(kb, n), rv = page_rsrc(vb, n);
 #pragma unroll
-        for (int t4 = 0; t4 < 2; ++t4)
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const auto x =
-                    __builtin_amdgcn_raw_buffer_load_b128(rk, koff + t4 * 4 * row_bytes + 256 * q, 0, 0);
-                p.k[t4][q] = make_uint4(x[0], x[1], x[2], x[3]);
-            }
-#pragma unroll
-        for (int t = 0; t < kHalf; ++t) {
-            const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + t * row_bytes, 0, 0);
-            p.v[t] = make_uint2(x[0], x[1]);
-        }
+    for (int t = 0; t < kHalf; ++t) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + t * row_bytes, 0, 0);
+        p.v[t] = make_uint2(x[0], x[1]);
     }
+}
+
+// A use of every register of a half page (no instructions): a wave that
+// skips a half page still waits for its loads there, so every path leaves
+// the ring's registers in the same state and the compiler's load-counter
+// waits stay exact (a path with loads still pending would make it wait for
+// all loads in flight wherever those registers are reused).
+__device__ __forceinline__ void consume(const HalfPage &p) {
+#pragma unroll
+    for (int t4 = 0; t4 < 2; ++t4)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) asm volatile("" ::"v"(p.k[t4][q].x), "v"(p.k[t4][q].y), "v"(p.k[t4][q].z), "v"(p.k[t4][q].w));
+#pragma unroll
+    for (int t = 0; t < kHalf; ++t) asm volatile("" ::"v"(p.v[t].x), "v"(p.v[t].y));
 }
 
 // m is the running max of the raw scores q.k; probabilities are
@@ -344,7 +340,7 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
     if (p_begin >= p_end) return;  // uniform over the workgroup
     const int hkv = a.num_kv_heads;
     const int nh = a.num_heads;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hl = wave >> 1;  // head within the workgroup
     const int half = wave & 1;  // tokens 8*half .. 8*half+7 of each page
     // This wave's kv head: grid.y splits the heads when more than fit one
@@ -545,7 +541,11 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
         __builtin_amdgcn_sched_barrier(0);
         const Cursor cur = cq[0];
         const int lim = lim_of(cur) - kHalf * half;  // valid tokens of this wave's half
-        if (lim > 0) compute_half<G>(st, cr, qv, r, j, min(lim, kHalf), p_lds + 32 * wave);
+        if (lim > 0) {
+            compute_half<G>(st, cr, qv, r, j, min(lim, kHalf), p_lds + 32 * wave);
+        } else {
+            consume(cr);
+        }
         if (!cq[1].ok || cq[1].b != cur.b) {
             finish(cur, cq[1].ok ? cq[1].b : 0);
             if (cq[1].ok) fill_q(cq[1].b);
