@@ -420,11 +420,26 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
 }
 
 // Merge the partials of units cut across workgroups: one workgroup per
-// (unit, 16 rows of the tile); thread = (row, 16-dim slice).
+// (unit, 16 rows of the tile); thread = (row, 16-dim slice).  Three memory
+// round trips: the unit's block range together with the search for its
+// sequence (a ballot over the unit prefix sums, no dependent loads), then
+// the sequence's token range, then every piece's (m, l) and acc slice,
+// requested before any is used and merged online.
 __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
+    constexpr int kMaxP = 4;  // pieces requested together
     const int u = blockIdx.x;
+    const int lane = threadIdx.x & 63;
     const int ub = a.mq_pre[u] + kMqUnitCost;  // the unit's first block
     const int ue = a.mq_pre[u + 1];
+    // Sequence of unit u: the number of sequences whose units end at or before u.
+    int b = 0;
+    for (int c0 = 0; c0 < a.n_seqs; c0 += 64) {
+        const int i = c0 + lane;
+        const uint64_t m = __ballot(i < a.n_seqs && a.upre[i + 1] <= u);
+        b += __popcll(m);
+        if (m != ~0ull) break;
+    }
+    b = __builtin_amdgcn_readfirstlane(b);
     if (ue <= ub) return;
     const int W = a.n_wg;
     const int NB = a.total_blocks;
@@ -434,7 +449,6 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int hkv = a.num_kv_heads;
     const int G = a.num_heads / hkv;
     const int Q = a.q_tile;
-    const int b = upper_index(a.upre, a.n_seqs, u);
     const int x = u - a.upre[b];
     const int tile = x / hkv;
     const int h = x - tile * hkv;
@@ -442,36 +456,58 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int d0 = (threadIdx.x & 15) * 16;
     const int iq = rho / G;
     const int gq = rho - iq * G;
-    const int T = a.tok_off[b + 1] - a.tok_off[b];
+    const int tok = a.tok_off[b];
+    const int T = a.tok_off[b + 1] - tok;
     const int qi = tile * Q + iq;
     if (iq >= Q || qi >= T) return;
-    float big = -INFINITY;
-    for (int ww = w0; ww <= w1; ++ww) {
-        const int slot = 2 * ww + (ub <= mq_wg_start(ww, NB, W) ? 0 : 1);
-        big = fmaxf(big, a.ws_ml[(static_cast<size_t>(slot) * kMqSlotRows + rho) * 2]);
-    }
-    const float mu = (big == -INFINITY) ? 0.0f : big;
-    float lt = 0.0f;
+    // Running merge: (big, lt, o) over the pieces so far; m in log2 units.
+    float big = -INFINITY, lt = 0.0f;
     float o[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[e] = 0.0f;
-    for (int ww = w0; ww <= w1; ++ww) {
-        const int slot = 2 * ww + (ub <= mq_wg_start(ww, NB, W) ? 0 : 1);
-        const size_t rowi = static_cast<size_t>(slot) * kMqSlotRows + rho;
-        const float c = __builtin_amdgcn_exp2f(a.ws_ml[rowi * 2] - mu);
-        lt += c * a.ws_ml[rowi * 2 + 1];
-        const float4 *src = reinterpret_cast<const float4 *>(a.ws_acc + rowi * kHeadDim + d0);
+    for (int wb = w0; wb <= w1; wb += kMaxP) {
+        float2 ml[kMaxP];
+        float4 v[kMaxP][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float4 v = src[e];
-            o[4 * e] += c * v.x;
-            o[4 * e + 1] += c * v.y;
-            o[4 * e + 2] += c * v.z;
-            o[4 * e + 3] += c * v.w;
+        for (int i = 0; i < kMaxP; ++i) {
+            const int ww = wb + i;
+            if (ww <= w1) {
+                const int slot = 2 * ww + (ub <= mq_wg_start(ww, NB, W) ? 0 : 1);
+                const size_t rowi = static_cast<size_t>(slot) * kMqSlotRows + rho;
+                ml[i] = *reinterpret_cast<const float2 *>(a.ws_ml + rowi * 2);
+                const float4 *src = reinterpret_cast<const float4 *>(a.ws_acc + rowi * kHeadDim + d0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][e] = src[e];
+            } else {
+                ml[i] = make_float2(-INFINITY, 0.0f);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][e] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
+        float nb = big;
+#pragma unroll
+        for (int i = 0; i < kMaxP; ++i) nb = fmaxf(nb, ml[i].x);
+        const float mu = (nb == -INFINITY) ? 0.0f : nb;  // rows that see no key of these pieces
+        const float keep = (big == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(big - mu);
+        lt *= keep;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] *= keep;
+#pragma unroll
+        for (int i = 0; i < kMaxP; ++i) {
+            const float c = (ml[i].x == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(ml[i].x - mu);
+            lt += c * ml[i].y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                o[4 * e] += c * v[i][e].x;
+                o[4 * e + 1] += c * v[i][e].y;
+                o[4 * e + 2] += c * v[i][e].z;
+                o[4 * e + 3] += c * v[i][e].w;
+            }
+        }
+        big = nb;
     }
     const float inv = 1.0f / lt;
-    uint16_t *orow = a.out + (static_cast<size_t>(a.tok_off[b] + qi) * a.num_heads + h * G + gq) * kHeadDim + d0;
+    uint16_t *orow = a.out + (static_cast<size_t>(tok + qi) * a.num_heads + h * G + gq) * kHeadDim + d0;
     uint4 o0, o1;
     o0.x = pack_h2(o[0] * inv, o[1] * inv);
     o0.y = pack_h2(o[2] * inv, o[3] * inv);
