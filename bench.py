@@ -20,7 +20,9 @@ numpy oracle on a bounded sample of the same workload on this host.
 
 Other workloads: --workload ctx8192 (every sequence at 8192 rows), c2
 (16 layers, B=1, 128 decode steps growing 128 -> 256 rows), c2graph (the
-same with the 16-layer step recorded once and replayed), copy (HBM
+same with the 16-layer step recorded once and replayed), c4 (chunked
+prefill), c5 (tree verify + rollback), proj (config 3 with its producer:
+the fused Q/K/V projection + append, then the gated decode), copy (HBM
 stream-copy probe: the measured bandwidth ceiling).
 """
 from __future__ import annotations
@@ -142,6 +144,80 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
         "decode_avg_us": float(np.mean(dec_ms) * 1e3), "decode_min_us": float(np.min(dec_ms) * 1e3),
         "split_tokens": split_used, "n_splits": n_splits,
     }
+
+
+def proj_workload(dev, steps, warmup, hidden=5120):
+    """The config-3 step with its producer: per layer, kva_project_append
+    (the Q+Q_gate and K+V projections of the 32 new tokens from hidden
+    5120, norm + RoPE, K/V into the pages) then kva_decode_gated.  Each
+    layer has its own weights (16 x 147 MB, so no layer's weights are still
+    cached when it comes round again); their values are a 32 MiB random
+    tile repeated on the device."""
+    spec = wl.c3_spec(0)
+    lengths, block_ids, n_blocks = spec.lengths, spec.block_ids, spec.n_blocks
+    B = len(lengths)
+    mbps = max(len(ids) for ids in block_ids)
+    cache = PagedKVCache(n_layers=LAYERS, max_seqs=B, max_blocks=n_blocks, max_blocks_per_seq=mbps,
+                         max_step_tokens=max(64, B))
+    for b, ids in enumerate(block_ids):
+        cache.set_blocks(b, ids)
+    cache.sync_tables()
+    fill_pools(dev, cache, n_blocks)
+    rows = int(max(lengths)) + 2
+    cos, sin = rope_tables(rows)
+    d_cos, d_sin = dev.array(cos), dev.array(sin)
+    rng = np.random.default_rng(2)
+    tile = (rng.standard_normal(16 * 1024 * 1024, dtype=np.float32) / np.sqrt(hidden)).astype(np.float16)
+    d_tile = dev.array(tile)
+    nq, nkv = 2 * H * D * hidden * 2, 2 * HKV * D * hidden * 2  # bytes
+    layers = []
+    for layer in range(LAYERS):
+        w = []
+        for nbytes in (nq, nkv):
+            d = dev.empty((nbytes // 2,), np.float16)
+            off = 0
+            while off < nbytes:
+                n = min(tile.nbytes - 4096 * layer, nbytes - off)
+                _lib.call("kva_memcpy_d2d", d.ptr + off, d_tile.ptr + 4096 * layer, n)
+                off += n
+            w.append(d)
+        x = dev.array(wl.normal_f16(rng, (B, hidden)))
+        qw, kw = dev.array(wl.norm_weight(rng)), dev.array(wl.norm_weight(rng))
+        q, g, out = (dev.empty((B, H, D), np.float16) for _ in range(3))
+        layers.append((x, w[0], w[1], qw, kw, q, g, out))
+    d_tile.free()
+    seqs, ones = list(range(B)), [1] * B
+
+    def step(evs=None):
+        for b in seqs:
+            cache.set_len(b, int(lengths[b]))
+        cache.begin_step(seqs, ones)
+        for layer, (x, wq, wkv, qw, kw, q, g, out) in enumerate(layers):
+            if evs is not None:
+                evs[layer][0].record()
+            cache.project_append(layer, x, hidden, wq, wkv, qw, kw, d_cos, d_sin, rows, q, g)
+            if evs is not None:
+                evs[layer][1].record()
+            cache.decode(layer, q, out, gate=g)
+            if evs is not None:
+                evs[layer][2].record()
+
+    for _ in range(warmup):
+        step()
+    dev.synchronize()
+    evs = [[[Event(), Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    proj_ms = [e[0].elapsed_ms(e[1]) for s_ in evs for e in s_]
+    dec_ms = [e[1].elapsed_ms(e[2]) for s_ in evs for e in s_]
+    cache.destroy()
+    alg = (nq + nkv) + B * hidden * 2 + 2 * B * H * D * 2 + B * 2 * HKV * D * 2
+    return {"wall_s": wall, "steps": steps, "B": B, "hidden": hidden, "alg_bytes_proj": alg,
+            "weight_bytes": nq + nkv, "proj_avg_us": float(np.mean(proj_ms) * 1e3),
+            "decode_avg_us": float(np.mean(dec_ms) * 1e3)}
 
 
 def c2_workload(dev, steps_unused, warmup, graph=False, split=0):
@@ -383,7 +459,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "c2graph", "c4", "c5", "copy"])
+    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "copy"])
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -412,6 +488,22 @@ def main() -> int:
                                      else "per-layer calls"}}))
         return 0
 
+    if args.workload == "proj":
+        r = proj_workload(dev, args.steps, args.warmup)
+        gbs = r["alg_bytes_proj"] / (r["proj_avg_us"] * 1e-6) / 1e9
+        ms = r["wall_s"] * 1e3 / r["steps"]
+        print(json.dumps({
+            "metric": "config-3 producer GB/s: fused Q/K/V projection + norm + RoPE + append (B=32, hidden 5120)",
+            "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
+            "config": {"workload": "C3 + producer", "layers": LAYERS, "batch": r["B"], "hidden": r["hidden"]},
+            "tok_per_s": r["B"] * r["steps"] / r["wall_s"], "decode_gated_avg_us": r["decode_avg_us"],
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("project_c3_traffic.json"),
+                         "kernel": "kva_project_append = proj_stream_kernel<2 token tiles, 8 waves, 7 row tiles, "
+                                   "10 k-steps, depth 8> + proj_finish_kernel",
+                         "avg_us": r["proj_avg_us"], "alg_bytes_per_launch": r["alg_bytes_proj"]}}))
+        return 0
     if args.workload == "c4":
         r = c4_workload(dev, args.steps, args.warmup)
         tflops = r["flops_per_layer"] / (r["prefill_avg_us"] * 1e-6) / 1e12

@@ -154,6 +154,29 @@ int kva_append_qknorm_rope(kva_cache *cache, int32_t layer, void *q, void *k,
                            const void *v, const void *q_norm_w, const void *k_norm_w,
                            const void *cos_tab, const void *sin_tab, int32_t table_rows,
                            kva_stream_t stream);
+/* The Q/K/V projection of every new token of the step, fused with the
+ * append above: the producer side of the cache.  Replaces the FP16
+ * attention projections (gemv_fp16_v2, gemv_fp16_v2.hip:22-85) launched at
+ * engine.py:2000-2022 (per sequence at :1815-1828; from the launch cache at
+ * :3367-3400 and c_dispatch.c:1042-1059, where V's GEMV writes into the
+ * cache slot) plus the norm/RoPE/append launches of kva_append_qknorm_rope.
+ * x: [T, hidden] fp16, the normed hidden states in step token order;
+ * hidden a multiple of 512.  w_q_fused: [2*num_heads*256, hidden] fp16, Q
+ * rows then Q_gate rows; w_kv_fused: [2*num_kv_heads*256, hidden] fp16, K
+ * rows then V rows (the stacked weights of engine.py:1366-1378).  Each
+ * projected value is the fp32 sum rounded to fp16 (what the reference's GEMV
+ * stores); Q and K are then normalised and rotated exactly as
+ * kva_append_qknorm_rope does, K and V go to the cache slots.  Outputs:
+ * q_out [T, num_heads, 256] (normalised + rotated Q, the input of
+ * kva_decode / kva_prefill / kva_tree_verify); q_gate_out [T, num_heads,
+ * 256] (Q_gate as projected, the gate of kva_decode_gated with gate_stride
+ * num_heads*256; may be NULL); kv_out [T, 2, num_kv_heads, 256] (K and V as
+ * projected, the reference's d_kv_fused; may be NULL).  16-byte aligned.   */
+int kva_project_append(kva_cache *cache, int32_t layer, const void *x, int32_t hidden,
+                       const void *w_q_fused, const void *w_kv_fused,
+                       const void *q_norm_w, const void *k_norm_w,
+                       const void *cos_tab, const void *sin_tab, int32_t table_rows,
+                       void *q_out, void *q_gate_out, void *kv_out, kva_stream_t stream);
 /* GQA decode attention, one query token per sequence (every n_new == 1):
  * out[b] = softmax(q[b] K^T / 16) V over the sequence's rows [0, len).
  * Replaces flash_attn_256_decode (flash_attn_256_tuned.hip:198-350) as

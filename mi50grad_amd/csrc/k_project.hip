@@ -1,0 +1,330 @@
+// Q/K/V projection fused with QK-RMSNorm + RoPE + K/V append (gfx950).
+//
+// The reference projects the normed hidden state with FP16 GEMVs
+// (gemv_fp16_v2.hip:22-85: fp32 accumulation, fp16 result) into [Q | Q_gate]
+// and [K | V] buffers (engine.py:1366-1378 stack the weights that way), then
+// normalises/rotates Q and K and copies K and V into the cache slot
+// (engine.py:2000-2022, 2371-2432; c_dispatch.c:1042-1059 sends V's GEMV
+// straight to the slot).  Here a step's tokens are projected together:
+//
+// proj_gemm_kernel: out[t][n] = sum_k W[n][k] x[t][k] as split-K MFMA tiles.
+//   A workgroup owns a run of 16-row weight tiles and one of `splits`
+//   slices of hidden; each of its waves takes an equal part of the slice for
+//   all those rows and all tokens (up to four 16-token column
+//   tiles), so every weight byte is read from HBM once and x (a few hundred
+//   KB) comes from L2.  The k order inside a 32-wide MFMA step is free as long
+//   as A and B agree: lane group g holds elements 8g..8g+7 of both, 16-byte
+//   loads, 64 contiguous bytes of each weight row per load.  A ring of
+//   register stages with fixed roles keeps several k-steps of loads in
+//   flight ahead of the MFMAs; the last round's extra slots reload cached
+//   weights against zero x instead of branching, so the compiler's
+//   load-counter waits never drain the loads in flight.  The waves' sums
+//   meet in LDS in a fixed order and go out as fp32 partials
+//   [split][token][row].
+// proj_finish_kernel: per (token, head), one 32-lane group sums the splits
+//   in order, rounds to fp16 and then does what the append kernel does:
+//   Q -> norm + RoPE -> q_out, Q_gate -> gate_out, K -> norm + RoPE -> its
+//   page slot, V -> its page slot (and K, V as projected -> kv_out).
+#include "k_common.h"
+#include "k_normrope.h"
+#include "kva_internal.h"
+
+namespace kva {
+namespace {
+
+__device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
+
+template <int NTB, int RT>
+struct ProjStage {
+    uint4 w[RT];   // 16-row weight tiles: row 16*i + lane%16, 8 elements
+    uint4 x[NTB];  // 16-token tiles: token 16*j + lane%16, the same 8 elements
+};
+
+// This workgroup's weight row tiles: tile i holds rows 16*(grp*RT + i) ..
+// +15 of the stacked [w_a; w_b] (a tile never straddles the two: n_a is a
+// multiple of 16).  Tiles past the last one repeat it (live = false: loaded,
+// never written), so every wave issues the same loads.  wt[i] points at
+// this lane's row and first element.
+template <int RT>
+__device__ __forceinline__ void proj_tiles(const ProjectArgs &a, int grp, int lane_off,
+                                           const uint16_t *(&wt)[RT], bool (&live)[RT]) {
+    const int n_t16 = (a.n_a + a.n_b) / 16;
+    const size_t hidden = static_cast<size_t>(a.hidden);
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        const int t16 = grp * RT + i;
+        live[i] = t16 < n_t16;
+        const int row = 16 * min(t16, n_t16 - 1);
+        const uint16_t *base = row < a.n_a ? a.w_a + static_cast<size_t>(row) * hidden
+                                           : a.w_b + static_cast<size_t>(row - a.n_a) * hidden;
+        wt[i] = base + lane_off;
+    }
+}
+
+// Sum the waves' k ranges, one row tile at a time through LDS, in wave
+// order; wave i % WAVES writes row tile i's partial [split][token][row].
+template <int NTB, int WAVES, int RT>
+__device__ __forceinline__ void proj_reduce_store(const ProjectArgs &a, float4_t (&acc)[RT][NTB],
+                                                  float4_t (&red)[WAVES][NTB][64], const bool (&live)[RT],
+                                                  int grp, int split, int wave, int lane) {
+    const size_t N = static_cast<size_t>(a.n_a) + a.n_b;
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+#pragma unroll
+        for (int j = 0; j < NTB; ++j) red[wave][j][lane] = acc[i][j];
+        __syncthreads();
+        if (wave == i % WAVES && live[i]) {
+#pragma unroll
+            for (int j = 0; j < NTB; ++j) {
+                float4_t sum = red[0][j][lane];
+#pragma unroll
+                for (int w = 1; w < WAVES; ++w) sum = sum + red[w][j][lane];
+                const int t = 16 * j + r;
+                if (t < a.n_tok) {
+                    float *dst = a.part + (static_cast<size_t>(split) * a.n_tok + t) * N +
+                                 16 * (grp * RT + i) + 4 * g;
+                    *reinterpret_cast<float4_t *>(dst) = sum;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Load k-step `step` of this wave into a stage.  Steps past the wave's
+// range (the ring's last round) reload the final step's weights (cache hits)
+// and read x out of range (zeros), so their MFMAs add nothing and every
+// round issues the same loads: no branch, exact load-counter waits.
+template <int NTB, int RT>
+__device__ __forceinline__ void proj_load(ProjStage<NTB, RT> &st, const uint16_t *const (&wt)[RT],
+                                          __amdgpu_buffer_rsrc_t xr, const uint32_t (&xoff)[NTB], int step,
+                                          int steps) {
+    const int ks = min(step, steps - 1);
+#pragma unroll
+    for (int i = 0; i < RT; ++i) st.w[i] = ld16(wt[i] + 32 * ks);
+#pragma unroll
+    for (int j = 0; j < NTB; ++j) {
+        const uint32_t off = step < steps ? xoff[j] + 64u * static_cast<uint32_t>(ks) : 0x80000000u;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+        st.x[j] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+template <int NTB, int RT>
+__device__ __forceinline__ void proj_mfma(float4_t (&acc)[RT][NTB], const ProjStage<NTB, RT> &st) {
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(st.w[i]), as_h8(st.x[j]), acc[i][j], 0, 0, 0);
+}
+
+// General form.  Grid: ceil(rows / (16 * RT)) * splits workgroups of WAVES
+// waves; each wave covers all 16 * RT rows of its workgroup for
+// hidden / (splits * WAVES) elements of k.  The host checks
+// hidden % (32 * WAVES * splits) == 0 and n_tok <= 16 * NTB.  A ring of
+// DEPTH + 1 stages keeps DEPTH k-steps of loads in flight while one is
+// multiplied.
+template <int NTB, int WAVES, int DEPTH, int RT>
+__global__ __launch_bounds__(64 * WAVES) void proj_gemm_kernel(ProjectArgs a) {
+    constexpr int R = DEPTH + 1;
+    __shared__ float4_t red[WAVES][NTB][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_grp = ((a.n_a + a.n_b) / 16 + RT - 1) / RT;
+    const int grp = blockIdx.x % n_grp;
+    const int split = blockIdx.x / n_grp;
+    const int steps = a.hidden / (32 * WAVES * a.splits);  // k-steps of this wave
+    const int k0 = (split * WAVES + wave) * steps * 32;
+    const int r = lane & 15, g = lane >> 4;
+    const uint16_t *wt[RT];
+    bool live[RT];
+    proj_tiles<RT>(a, grp, r * a.hidden + k0 + 8 * g, wt, live);
+    // x rows past n_tok lie outside the resource and load as zeros.
+    const auto xr = ro_rsrc(a.x, static_cast<uint32_t>(a.n_tok) * static_cast<uint32_t>(a.hidden) * 2u);
+    uint32_t xoff[NTB];
+#pragma unroll
+    for (int j = 0; j < NTB; ++j) xoff[j] = ((16 * j + r) * static_cast<uint32_t>(a.hidden) + k0 + 8 * g) * 2u;
+
+    float4_t acc[RT][NTB];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Slot j of round rr holds step rr*R + j.  Scheduling barriers keep each
+    // group of loads ahead of the MFMAs after it; left alone, the scheduler
+    // interleaves them and only a few loads stay in flight.
+    ProjStage<NTB, RT> st[R];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) {
+        __builtin_amdgcn_sched_barrier(0);
+        proj_load(st[j], wt, xr, xoff, j, steps);
+    }
+    const int rounds = (steps + R - 1) / R;
+    for (int rr = 0; rr < rounds; ++rr) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            __builtin_amdgcn_sched_barrier(0);
+            proj_load(st[(j + DEPTH) % R], wt, xr, xoff, rr * R + j + DEPTH, steps);
+            __builtin_amdgcn_sched_barrier(0);
+            proj_mfma(acc, st[j]);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    proj_reduce_store<NTB, WAVES, RT>(a, acc, red, live, grp, split, wave, lane);
+}
+
+// The form for up to 32 tokens and STEPS k-steps per wave: each wave's x
+// slice stays in registers for the whole kernel (loaded once at the start)
+// and the weights stream one row tile at a time, DEPTH loads along k ahead
+// of the MFMAs, so the loads in flight cover a few rows far along k
+// (contiguous bytes per row) rather than many rows one step deep.  The loop
+// over (row tile, k-step) is fully unrolled: every ring slot keeps a fixed
+// register.
+template <int NTB, int WAVES, int RT, int STEPS, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void proj_stream_kernel(ProjectArgs a) {
+    constexpr int N_LD = RT * STEPS;   // weight loads of a wave
+    constexpr int R = DEPTH + 1;
+    __shared__ float4_t red[WAVES][NTB][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_grp = ((a.n_a + a.n_b) / 16 + RT - 1) / RT;
+    const int grp = blockIdx.x % n_grp;
+    const int split = blockIdx.x / n_grp;
+    const int k0 = (split * WAVES + wave) * STEPS * 32;
+    const int r = lane & 15, g = lane >> 4;
+    const uint16_t *wt[RT];
+    bool live[RT];
+    proj_tiles<RT>(a, grp, r * a.hidden + k0 + 8 * g, wt, live);
+    const auto xr = ro_rsrc(a.x, static_cast<uint32_t>(a.n_tok) * static_cast<uint32_t>(a.hidden) * 2u);
+
+    uint4 xv[STEPS][NTB];
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j) {
+            const uint32_t off = ((16 * j + r) * static_cast<uint32_t>(a.hidden) + k0 + 8 * g + 32 * st) * 2u;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+            xv[st][j] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    float4_t acc[RT][NTB];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    uint4 ring[R];
+#pragma unroll
+    for (int n = 0; n < DEPTH; ++n) {
+        __builtin_amdgcn_sched_barrier(0);
+        ring[n] = ld16(wt[n / STEPS] + 32 * (n % STEPS));
+    }
+#pragma unroll
+    for (int n = 0; n < N_LD; ++n) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (n + DEPTH < N_LD) {  // resolved at compile time after unrolling
+            const int m = n + DEPTH;
+            ring[m % R] = ld16(wt[m / STEPS] + 32 * (m % STEPS));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const int i = n / STEPS, st = n % STEPS;
+#pragma unroll
+        for (int j = 0; j < NTB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(ring[n % R]), as_h8(xv[st][j]), acc[i][j], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    proj_reduce_store<NTB, WAVES, RT>(a, acc, red, live, grp, split, wave, lane);
+}
+
+// Grid: (token, block of 8 head rows) per 256-thread workgroup; one 32-lane
+// group per head row.  Head rows of a token: H query, H gate, Hkv key, Hkv
+// value heads (the order of the weight rows).  The token's metadata and
+// page id are workgroup-uniform, read through the scalar cache while the
+// partials are in flight.
+__global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
+    const int H = a.num_heads, hkv = a.num_kv_heads;
+    const int rows_per_tok = 2 * H + 2 * hkv;
+    const int blocks_per_tok = (rows_per_tok + 7) / 8;
+    const int tc = blockIdx.x / blocks_per_tok;
+    const int hr = (blockIdx.x - tc * blocks_per_tok) * 8 + (threadIdx.x >> 5);
+    const int lane = threadIdx.x & 31;
+    if (hr >= rows_per_tok) return;  // whole 32-lane group leaves
+    const int t = a.tok0 + tc;
+    const int pos = ld_uniform(a.tok_pos + t);
+    const int seq = ld_uniform(a.tok_seq + t);
+    const int slot = ld_uniform(a.tok_slot + t);
+    const int blk = ld_uniform(a.table + static_cast<size_t>(seq) * a.table_stride + (slot >> 4));
+    // Every split's partial is loaded at once (splits past a.splits reread
+    // split 0 and are not added), then summed in split order.
+    const size_t N = static_cast<size_t>(a.n_a) + a.n_b;
+    const size_t split_stride = static_cast<size_t>(a.n_tok) * N;
+    const float *p = a.part + static_cast<size_t>(tc) * N + static_cast<size_t>(hr) * kHeadDim + 8 * lane;
+    float4_t plo[kProjMaxSplits], phi[kProjMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kProjMaxSplits; ++s) {
+        const float *ps = p + (s < a.splits ? s : 0) * split_stride;
+        plo[s] = *reinterpret_cast<const float4_t *>(ps);
+        phi[s] = *reinterpret_cast<const float4_t *>(ps + 4);
+    }
+    float4_t lo = plo[0], hi = phi[0];
+#pragma unroll
+    for (int s = 1; s < kProjMaxSplits; ++s) {
+        lo = s < a.splits ? lo + plo[s] : lo;
+        hi = s < a.splits ? hi + phi[s] : hi;
+    }
+    uint4 y;
+    y.x = pack_h2(lo[0], lo[1]);
+    y.y = pack_h2(lo[2], lo[3]);
+    y.z = pack_h2(hi[0], hi[1]);
+    y.w = pack_h2(hi[2], hi[3]);
+
+    const uint16_t *cos_row = a.cos_tab + static_cast<size_t>(pos) * a.half_rot;
+    const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
+    if (hr < H) {
+        const uint4 q = norm_rope_row<32>(y, a.q_w, cos_row, sin_row, a.half_rot, a.eps, lane);
+        st16(a.q_out + (static_cast<size_t>(t) * H + hr) * kHeadDim + 8 * lane, q);
+        return;
+    }
+    if (hr < 2 * H) {
+        if (a.gate_out) st16(a.gate_out + (static_cast<size_t>(t) * H + hr - H) * kHeadDim + 8 * lane, y);
+        return;
+    }
+    const int kv = hr - 2 * H;  // 0..2*Hkv-1: K heads, then V heads
+    if (a.kv_out) st16(a.kv_out + (static_cast<size_t>(t) * 2 * hkv + kv) * kHeadDim + 8 * lane, y);
+    const size_t row_base = (static_cast<size_t>(blk) * kBlockTokens + (slot & 15)) * hkv;
+    if (kv < hkv) {
+        const uint4 k = norm_rope_row<32>(y, a.k_w, cos_row, sin_row, a.half_rot, a.eps, lane);
+        st16(a.k_pool + (row_base + kv) * kHeadDim + 8 * lane, k);
+    } else {
+        st16(a.v_pool + (row_base + kv - hkv) * kHeadDim + 8 * lane, y);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
+    if (a.n_tok <= 0) return hipSuccess;
+    constexpr int W = kProjWaves, P = kProjDepth, RT = kProjRowTiles;
+    const int n_grp = ((a.n_a + a.n_b) / 16 + RT - 1) / RT;
+    const dim3 grid(static_cast<unsigned>(n_grp * a.splits));
+    const dim3 block(64 * W);
+    const int ntb = (a.n_tok + 15) / 16;
+    if (ntb <= 2 && a.hidden == kProjStreamSteps * 32 * W * a.splits) {
+        constexpr int ST = kProjStreamSteps, SD = kProjStreamDepth;
+        if (ntb == 1) hipLaunchKernelGGL((proj_stream_kernel<1, W, RT, ST, SD>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((proj_stream_kernel<2, W, RT, ST, SD>), grid, block, 0, s, a);
+    } else switch (ntb) {
+        case 1: hipLaunchKernelGGL((proj_gemm_kernel<1, W, P, RT>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((proj_gemm_kernel<2, W, P, RT>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((proj_gemm_kernel<3, W, P, RT>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((proj_gemm_kernel<4, W, P, RT>), grid, block, 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    const int blocks_per_tok = (2 * a.num_heads + 2 * a.num_kv_heads + 7) / 8;
+    hipLaunchKernelGGL(proj_finish_kernel, dim3(a.n_tok * blocks_per_tok), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace kva

@@ -74,6 +74,8 @@ struct kva_cache {
     float *d_mq_acc = nullptr;  // multi-query partial slots [2*mq_max_wg][8][16][256]
     float *d_mq_ml = nullptr;
     int32_t mq_max_wg = 0;
+    float *d_proj = nullptr;    // projection partials [kProjMaxSplits][kProjTokens][(2H+2Hkv)*256]
+    size_t proj_floats = 0;
     int32_t max_wg = 0;  // decode workgroups the partial workspace can serve
     size_t ws_rows = 0;  // 256-float rows in the decode partial workspace
     int32_t n_cu = 0;
@@ -377,6 +379,11 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
             return cleanup(hip_fail(e, "hipMalloc(multi-query workspace)"));
         if ((e = hipMalloc(&c->d_mq_ml, mq_rows * 2 * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(multi-query workspace ml)"));
+        // Projection partials: every split of one launch pair's tokens.
+        c->proj_floats = static_cast<size_t>(kva::kProjMaxSplits) * kva::kProjTokens *
+                         (2 * static_cast<size_t>(cfg->num_heads) + 2 * cfg->num_kv_heads) * kva::kHeadDim;
+        if ((e = hipMalloc(&c->d_proj, c->proj_floats * sizeof(float))) != hipSuccess)
+            return cleanup(hip_fail(e, "hipMalloc(projection workspace)"));
         for (int i = 0; i < kStageSlots; ++i) {
             if ((e = hipHostMalloc(reinterpret_cast<void **>(&c->h_stage[i]), c->stage_bytes,
                                    hipHostMallocDefault)) != hipSuccess)
@@ -408,6 +415,7 @@ int kva_destroy(kva_cache *c) {
         (void)hipFree(c->d_ws_ml);
         (void)hipFree(c->d_mq_acc);
         (void)hipFree(c->d_mq_ml);
+        (void)hipFree(c->d_proj);
     }
     delete c;
     return KVA_OK;
@@ -773,6 +781,81 @@ static int append_impl(kva_cache *c, int32_t layer, void *q, void *k, const void
     return KVA_OK;
 }
 
+// Hidden split among projection workgroups: the most splits (up to
+// kProjMaxSplits) that give every wave a whole number of 32-wide k-steps
+// and keep the grid within kProjWgPerCu workgroups per CU (at hidden 5120,
+// 24 + 4 heads and 256 CUs: 128 row groups x 2 splits, one per CU).
+static int32_t project_splits(const kva_cache *c, int32_t hidden, int32_t n_rows) {
+    const int64_t n_grp = (n_rows / 16 + kva::kProjRowTiles - 1) / kva::kProjRowTiles;
+    int32_t best = 1;
+    for (int32_t s = 2; s <= kva::kProjMaxSplits; s *= 2)
+        if (hidden % (s * 32 * kva::kProjWaves) == 0 &&
+            n_grp * s <= static_cast<int64_t>(kva::kProjWgPerCu) * c->n_cu)
+            best = s;
+    return best;
+}
+
+static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidden, const void *w_q_fused,
+                        const void *w_kv_fused, const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                        const void *sin_tab, int32_t table_rows, void *q_out, void *q_gate_out, void *kv_out,
+                        kva_stream_t stream) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    if (c->st_n_tok == 0) return KVA_OK;
+    if (!x || !w_q_fused || !w_kv_fused || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out)
+        return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
+    if (!aligned16(x) || !aligned16(w_q_fused) || !aligned16(w_kv_fused) || !aligned16(q_norm_w) ||
+        !aligned16(k_norm_w) || !aligned16(q_out) || !aligned16(q_gate_out) || !aligned16(kv_out))
+        return fail(KVA_ERR_MISALIGNED, "x, weights, norm weights and outputs must be 16-byte aligned");
+    if (hidden <= 0 || hidden % kva::kProjHiddenQuantum != 0)
+        return fail(KVA_ERR_INVALID_ARG, "hidden %d must be a positive multiple of %d", hidden,
+                    kva::kProjHiddenQuantum);
+    if (static_cast<int64_t>(kva::kProjTokens) * hidden * 2 > INT32_MAX)
+        return fail(KVA_ERR_INVALID_ARG, "hidden %d too large", hidden);
+    const int half_rot = c->cfg.rotary_dim / 2;
+    if (half_rot > 0 && ((reinterpret_cast<uintptr_t>(cos_tab) | reinterpret_cast<uintptr_t>(sin_tab)) & 7u))
+        return fail(KVA_ERR_MISALIGNED, "cos/sin tables must be 8-byte aligned");
+    if (c->st_max_pos >= table_rows)
+        return fail(KVA_ERR_INVALID_ARG, "RoPE position %d beyond the %d table rows", c->st_max_pos,
+                    table_rows);
+    kva::ProjectArgs a{};
+    a.w_a = static_cast<const uint16_t *>(w_q_fused);
+    a.w_b = static_cast<const uint16_t *>(w_kv_fused);
+    a.n_a = 2 * c->cfg.num_heads * kva::kHeadDim;
+    a.n_b = 2 * c->cfg.num_kv_heads * kva::kHeadDim;
+    a.hidden = hidden;
+    a.splits = project_splits(c, hidden, a.n_a + a.n_b);
+    a.part = c->d_proj;
+    a.q_out = static_cast<uint16_t *>(q_out);
+    a.gate_out = static_cast<uint16_t *>(q_gate_out);
+    a.kv_out = static_cast<uint16_t *>(kv_out);
+    a.q_w = static_cast<const uint16_t *>(q_norm_w);
+    a.k_w = static_cast<const uint16_t *>(k_norm_w);
+    a.cos_tab = static_cast<const uint16_t *>(cos_tab);
+    a.sin_tab = static_cast<const uint16_t *>(sin_tab);
+    a.k_pool = c->d_k + c->layer_elems * layer;
+    a.v_pool = c->d_v + c->layer_elems * layer;
+    a.table = c->d_table;
+    a.table_stride = c->cfg.max_blocks_per_seq;
+    a.tok_seq = at<int32_t>(c->d_step, c->off_tseq);
+    a.tok_slot = at<int32_t>(c->d_step, c->off_tslot);
+    a.tok_pos = at<int32_t>(c->d_step, c->off_tpos);
+    a.num_heads = c->cfg.num_heads;
+    a.num_kv_heads = c->cfg.num_kv_heads;
+    a.half_rot = half_rot;
+    a.eps = c->cfg.eps;
+    const auto *xs = static_cast<const uint16_t *>(x);
+    for (int32_t t0 = 0; t0 < c->st_n_tok; t0 += kva::kProjTokens) {
+        a.tok0 = t0;
+        a.n_tok = std::min(kva::kProjTokens, c->st_n_tok - t0);
+        a.x = xs + static_cast<size_t>(t0) * hidden;
+        KVA_HIP(kva::launch_project(a, static_cast<hipStream_t>(stream)));
+    }
+    return KVA_OK;
+}
+
 int kva_set_decode_split(kva_cache *c, int32_t split_tokens) {
     if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
     if (split_tokens < 0 || split_tokens % kva::kSplitQuantum != 0)
@@ -858,6 +941,19 @@ int kva_append_qknorm_rope(kva_cache *c, int32_t layer, void *q, void *k, const 
     int rc = capture_check(c, stream);
     if (rc) return capture_note(c, rc);
     rc = append_impl(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, stream);
+    if (rc == KVA_OK && c->capturing && c->st_n_tok > 0)
+        c->cap_table_rows = c->cap_table_rows ? std::min(c->cap_table_rows, table_rows) : table_rows;
+    return capture_note(c, rc);
+}
+
+int kva_project_append(kva_cache *c, int32_t layer, const void *x, int32_t hidden, const void *w_q_fused,
+                       const void *w_kv_fused, const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                       const void *sin_tab, int32_t table_rows, void *q_out, void *q_gate_out, void *kv_out,
+                       kva_stream_t stream) {
+    int rc = capture_check(c, stream);
+    if (rc) return capture_note(c, rc);
+    rc = project_impl(c, layer, x, hidden, w_q_fused, w_kv_fused, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows,
+                      q_out, q_gate_out, kv_out, stream);
     if (rc == KVA_OK && c->capturing && c->st_n_tok > 0)
         c->cap_table_rows = c->cap_table_rows ? std::min(c->cap_table_rows, table_rows) : table_rows;
     return capture_note(c, rc);

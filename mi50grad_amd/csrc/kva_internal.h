@@ -39,6 +39,52 @@ struct AppendArgs {
 };
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
 
+// Q/K/V projection of a step's tokens fused with norm + RoPE + K/V append.
+// Weight rows: w_a = [Q heads | Q_gate heads] (n_a = 2*H*256 rows), w_b =
+// [K heads | V heads] (n_b = 2*Hkv*256 rows), each row `hidden` fp16.  One
+// launch pair covers up to kProjTokens tokens: proj_gemm_kernel writes
+// split-K fp32 partials, proj_finish_kernel sums them in split order, rounds
+// to fp16 (the projection the reference's GEMV stores) and finishes each head.
+constexpr int kProjTokens = 64;     // tokens per launch pair (4 MFMA column tiles)
+constexpr int kProjMaxSplits = 4;   // hidden split among workgroups, at most
+constexpr int kProjWaves = 8;       // waves per GEMM workgroup
+constexpr int kProjRowTiles = 7;    // 16-row weight tiles per GEMM workgroup
+constexpr int kProjDepth = 1;       // k-steps of loads in flight per wave (general form)
+constexpr int kProjHiddenQuantum = 512;  // hidden must be a multiple of this
+constexpr int kProjWgPerCu = 1;     // GEMM workgroups per CU the split aims for, at most
+constexpr int kProjStreamSteps = 10;  // k-steps per wave of the x-resident form (up to 32 tokens)
+constexpr int kProjStreamDepth = 8;   // weight loads in flight per wave there
+struct ProjectArgs {
+    const uint16_t *x;        // [n_tok][hidden], this chunk's first token
+    const uint16_t *w_a;
+    const uint16_t *w_b;
+    int32_t n_a, n_b;
+    int32_t hidden;
+    int32_t n_tok;            // tokens of this chunk, 1..kProjTokens
+    int32_t splits;
+    float *part;              // [splits][n_tok][n_a + n_b]
+    int32_t tok0;             // the chunk's first token within the step
+    uint16_t *q_out;          // [T][H][256]: normalised + rotated Q
+    uint16_t *gate_out;       // [T][H][256]: Q_gate as projected (nullable)
+    uint16_t *kv_out;         // [T][2][Hkv][256]: K, V as projected (nullable)
+    const uint16_t *q_w;
+    const uint16_t *k_w;
+    const uint16_t *cos_tab;
+    const uint16_t *sin_tab;
+    uint16_t *k_pool;
+    uint16_t *v_pool;
+    const int32_t *table;
+    int32_t table_stride;
+    const int32_t *tok_seq;
+    const int32_t *tok_slot;
+    const int32_t *tok_pos;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t half_rot;
+    float eps;
+};
+hipError_t launch_project(const ProjectArgs &a, hipStream_t s);
+
 // Reference-compatible norm+RoPE on a contiguous [n_heads][head_dim] buffer.
 struct LegacyNormArgs {
     uint16_t *x;

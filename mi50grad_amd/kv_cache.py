@@ -25,7 +25,9 @@ HEAD_DIM = 256
 
 
 def _ptr(x) -> int:
-    """Device address of an int pointer or a DeviceArray."""
+    """Device address of an int pointer or a DeviceArray (None stays NULL)."""
+    if x is None:
+        return None
     return x if isinstance(x, int) else x.ptr
 
 
@@ -145,6 +147,17 @@ class PagedKVCache:
                stream=None) -> None:
         _lib.call("kva_append_qknorm_rope", self.handle, layer, _ptr(q), _ptr(k), _ptr(v),
                   _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab), table_rows, stream)
+
+    def project_append(self, layer: int, x, hidden: int, w_q_fused, w_kv_fused, q_norm_w, k_norm_w,
+                       cos_tab, sin_tab, table_rows: int, q_out, q_gate_out=None, kv_out=None,
+                       stream=None) -> None:
+        """Q/K/V projection of the step's tokens fused with norm + RoPE +
+        append (the reference's FP16 GEMVs, engine.py:2000-2022, followed by
+        its norm/RoPE/cache-write launches).  Writes q_out [T, H, 256] and,
+        when given, q_gate_out [T, H, 256] and kv_out [T, 2, Hkv, 256]."""
+        _lib.call("kva_project_append", self.handle, layer, _ptr(x), hidden, _ptr(w_q_fused),
+                  _ptr(w_kv_fused), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab),
+                  table_rows, _ptr(q_out), _ptr(q_gate_out), _ptr(kv_out), stream)
 
     def decode(self, layer: int, q, out, stream=None, gate=None, gate_stride: int = 0) -> None:
         """Decode attention; with `gate`, the output gate (out *= sigmoid(gate),

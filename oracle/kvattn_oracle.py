@@ -54,6 +54,49 @@ def rope_tables(max_seq: int, head_dim: int = HEAD_DIM,
 
 
 # ---------------------------------------------------------------------------
+# producer: the FP16 attention projections
+# ---------------------------------------------------------------------------
+def project_fp16(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """out[t, n] = fp16(sum_k w[n, k] x[t, k]): the FP16 GEMV of
+    gemv_fp16_v2.hip:22-85 (fp16 operands, fp32 accumulation, one fp16
+    rounding of the sum) for every row t of x.
+
+    The sum is taken in float64, in which every fp16 product is exact, so
+    the result is the correctly rounded fp16 of a sum whose own error is far
+    below the fp32 accumulation error of any GPU summation order: a GPU
+    result may differ from this by at most one fp16 ulp, and by none when
+    every partial sum is exactly representable in fp32.
+    """
+    acc = np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
+    return acc.astype(np.float16)
+
+
+def project_append(x, w_q_fused, w_kv_fused, q_w, k_w, cos_rows, sin_rows,
+                   num_heads: int = NUM_HEADS, num_kv_heads: int = NUM_KV_HEADS):
+    """The reference's producer for one step, token by token: the Q+Q_gate
+    and K+V GEMVs (engine.py:2000-2022 over the stacked weights of
+    engine.py:1366-1378), then QK-norm + RoPE of Q and K
+    (engine.py:2371-2432).  Returns (q [T,H,256] normed + rotated,
+    q_gate [T,H,256], k_raw [T,Hkv,256], k [T,Hkv,256] normed + rotated,
+    v [T,Hkv,256])."""
+    T = x.shape[0]
+    qd, kd = num_heads * HEAD_DIM, num_kv_heads * HEAD_DIM
+    qf = project_fp16(x, w_q_fused)
+    kvf = project_fp16(x, w_kv_fused)
+    q_raw = qf[:, :qd].reshape(T, num_heads, HEAD_DIM)
+    gate = qf[:, qd:].reshape(T, num_heads, HEAD_DIM)
+    k_raw = kvf[:, :kd].reshape(T, num_kv_heads, HEAD_DIM)
+    v = kvf[:, kd:].reshape(T, num_kv_heads, HEAD_DIM)
+    cq = np.repeat(cos_rows, num_heads, axis=0)
+    sq = np.repeat(sin_rows, num_heads, axis=0)
+    q = qknorm_rope_exact(q_raw.reshape(-1, HEAD_DIM), q_w, cq, sq).reshape(T, num_heads, HEAD_DIM)
+    ck = np.repeat(cos_rows, num_kv_heads, axis=0)
+    sk = np.repeat(sin_rows, num_kv_heads, axis=0)
+    k = qknorm_rope_exact(k_raw.reshape(-1, HEAD_DIM), k_w, ck, sk).reshape(T, num_kv_heads, HEAD_DIM)
+    return q, gate, k_raw, k, v
+
+
+# ---------------------------------------------------------------------------
 # a2/a3: fused per-head RMSNorm + interleaved partial RoPE
 # ---------------------------------------------------------------------------
 def qknorm_rope_exact(x: np.ndarray, w: np.ndarray, cos_rows: np.ndarray,

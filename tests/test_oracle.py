@@ -344,3 +344,75 @@ def test_sigmoid_gate_pins():
     ref = (out.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))).astype(np.float16)
     diff = np.abs(orc.sigmoid_gate(out, g).astype(np.float64) - ref.astype(np.float64))
     assert np.all(diff <= np.abs(ref.astype(np.float64)) * 2.0 ** -10 + 1e-7)
+
+
+# ---------------------------------------------------------------- projection
+def _project_fraction(x, w):
+    """Exact rational sum per output, then one fp16 rounding (brute force)."""
+    from fractions import Fraction
+
+    T, K = x.shape
+    N = w.shape[0]
+    out = np.empty((T, N), np.float16)
+    for t in range(T):
+        xs = [Fraction(float(v)) for v in x[t]]
+        for n in range(N):
+            acc = sum((Fraction(float(w[n, k])) * xs[k] for k in range(K)), Fraction(0))
+            out[t, n] = np.float16(float(acc))
+    return out
+
+
+def test_project_fp16_pins():
+    """gemv_fp16_v2.hip:22-85 restated: exact rational brute force on small
+    cases (a transposed operand or a dropped term fails it), unit rows pick
+    single elements, and fp32-exact integer sums survive any order."""
+    rng = np.random.default_rng(5)
+    for T, K, N in ((1, 64, 8), (3, 32, 5), (2, 96, 7)):
+        x = rng.standard_normal((T, K)).astype(np.float16)
+        w = (rng.standard_normal((N, K)) * 0.2).astype(np.float16)
+        assert np.array_equal(orc.project_fp16(x, w).view(np.uint16), _project_fraction(x, w).view(np.uint16))
+        assert not np.array_equal(orc.project_fp16(x, w[::-1]), _project_fraction(x, w))
+    x = rng.standard_normal((4, 512)).astype(np.float16)
+    pick = rng.integers(0, 512, 40)
+    w = np.zeros((40, 512), np.float16)
+    w[np.arange(40), pick] = 1
+    assert np.array_equal(orc.project_fp16(x, w).view(np.uint16), x[:, pick].view(np.uint16))
+    # Integer products of magnitude <= 6 * 2^-7 summed over 5120 terms stay
+    # exact in fp32: the sum is order independent and equals the fp32 sum.
+    xi = rng.integers(-3, 4, (2, 5120)).astype(np.float16)
+    wi = (rng.integers(-2, 3, (16, 5120)) * 2.0 ** -7).astype(np.float16)
+    f32 = np.zeros((2, 16), np.float32)
+    for k in range(0, 5120, 512):
+        f32 += xi[:, k:k + 512].astype(np.float32) @ wi[:, k:k + 512].astype(np.float32).T
+    assert np.array_equal(orc.project_fp16(xi, wi).view(np.uint16), f32.astype(np.float16).view(np.uint16))
+
+
+def test_project_append_layout():
+    """The producer composite reads the stacked weights the reference's way
+    (engine.py:1366-1378: Q rows then Q_gate rows, K rows then V rows) and
+    hands Q and K to the pinned norm + RoPE.  Unit-row weights make every
+    projected value a known element of x, so a swapped half or head order
+    shows up as a wrong element."""
+    rng = np.random.default_rng(6)
+    H, HKV, D, K, T = 2, 1, 256, 512, 3
+    x = rng.standard_normal((T, K)).astype(np.float16)
+    wq = np.zeros((2 * H * D, K), np.float16)
+    wkv = np.zeros((2 * HKV * D, K), np.float16)
+    sq = rng.integers(0, K, 2 * H * D)
+    skv = rng.integers(0, K, 2 * HKV * D)
+    wq[np.arange(2 * H * D), sq] = 1
+    wkv[np.arange(2 * HKV * D), skv] = 1
+    qw = (1 + 0.02 * rng.standard_normal(D)).astype(np.float16)
+    kw = (1 + 0.02 * rng.standard_normal(D)).astype(np.float16)
+    cos, sin = orc.rope_tables(64)
+    pos = np.array([5, 17, 40])
+    q, gate, k_raw, k, v = orc.project_append(x, wq, wkv, qw, kw, cos[pos], sin[pos], H, HKV)
+    q_raw = x[:, sq[:H * D]].reshape(T, H, D)
+    assert np.array_equal(gate.view(np.uint16), x[:, sq[H * D:]].reshape(T, H, D).view(np.uint16))
+    assert np.array_equal(k_raw.view(np.uint16), x[:, skv[:HKV * D]].reshape(T, HKV, D).view(np.uint16))
+    assert np.array_equal(v.view(np.uint16), x[:, skv[HKV * D:]].reshape(T, HKV, D).view(np.uint16))
+    for h in range(H):
+        exp = orc.qknorm_rope_exact(q_raw[:, h], qw, cos[pos], sin[pos])
+        assert np.array_equal(q[:, h].view(np.uint16), exp.view(np.uint16))
+    exp = orc.qknorm_rope_exact(k_raw[:, 0], kw, cos[pos], sin[pos])
+    assert np.array_equal(k[:, 0].view(np.uint16), exp.view(np.uint16))
