@@ -500,8 +500,8 @@ def main() -> int:
             "tok_per_s": r["B"] * r["steps"] / r["wall_s"], "decode_gated_avg_us": r["decode_avg_us"],
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("project_c3_traffic.json"),
-                         "kernel": "kva_project_append = proj_stream_kernel<2 token tiles, 8 waves, 7 row tiles, "
-                                   "10 k-steps, depth 8> + proj_finish_kernel",
+                         "kernel": "kva_project_append = proj_lds_kernel<2 token tiles, 8 waves, 7 row tiles, "
+                                   "10 k-steps, 6 stages> + proj_finish_kernel",
                          "avg_us": r["proj_avg_us"], "alg_bytes_per_launch": r["alg_bytes_proj"]}}))
         return 0
     if args.workload == "c4":

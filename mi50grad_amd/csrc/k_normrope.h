@@ -14,13 +14,39 @@
 
 namespace kva {
 
+// The operands a row's norm + RoPE reads besides the row itself: this
+// lane's 8 norm weights and its 4 cos/sin pairs.  Loaded apart from the
+// math so a kernel can request them before it waits for the row.
+struct NormRopeIn {
+    uint4 w;
+    uint2 c, s;
+};
+
+// Lanes past LANES get zero weights; lanes past the rotary pairs read the
+// last lane's cos/sin (in bounds, never used).  half_rot % 4 == 0.
+template <int LANES>
+__device__ __forceinline__ NormRopeIn norm_rope_in(const uint16_t *__restrict__ w,
+                                                   const uint16_t *__restrict__ cos_row,
+                                                   const uint16_t *__restrict__ sin_row, int half_rot,
+                                                   int lane) {
+    NormRopeIn in;
+    in.w = (lane < LANES) ? ld16(w + 8 * lane) : make_uint4(0, 0, 0, 0);
+    if (half_rot > 0) {
+        const int cl = min(lane, half_rot / 4 - 1);
+        in.c = ld8(cos_row + 4 * cl);
+        in.s = ld8(sin_row + 4 * cl);
+    } else {
+        in.c = make_uint2(0, 0);
+        in.s = make_uint2(0, 0);
+    }
+    return in;
+}
+
 // Normalise + rotate one row held as 8 fp16 per lane.  LANES = head_dim / 8
 // lanes take part (lane < LANES); the butterfly stays inside them.
 template <int LANES>
-__device__ __forceinline__ uint4 norm_rope_row(uint4 xin, const uint16_t *__restrict__ w,
-                                               const uint16_t *__restrict__ cos_row,
-                                               const uint16_t *__restrict__ sin_row,
-                                               int half_rot, float eps, int lane) {
+__device__ __forceinline__ uint4 norm_rope_apply(uint4 xin, const NormRopeIn &in, int half_rot, float eps,
+                                                 int lane) {
 #pragma clang fp contract(off)
     const uint32_t xw[4] = {xin.x, xin.y, xin.z, xin.w};
     float x[8];
@@ -44,8 +70,7 @@ __device__ __forceinline__ uint4 norm_rope_row(uint4 xin, const uint16_t *__rest
     const float var = ms + eps;
     const float inv = 1.0f / sqrtf(var);
 
-    const uint4 wv = (lane < LANES) ? ld16(w + 8 * lane) : make_uint4(0, 0, 0, 0);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    const uint32_t ww[4] = {in.w.x, in.w.y, in.w.z, in.w.w};
     float n[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -56,10 +81,8 @@ __device__ __forceinline__ uint4 norm_rope_row(uint4 xin, const uint16_t *__rest
     }
     if (8 * lane < 2 * half_rot) {
         // This lane holds pairs 4*lane .. 4*lane+3.
-        const uint2 cv = ld8(cos_row + 4 * lane);
-        const uint2 sv = ld8(sin_row + 4 * lane);
-        const float c[4] = {lo_f(cv.x), hi_f(cv.x), lo_f(cv.y), hi_f(cv.y)};
-        const float sn[4] = {lo_f(sv.x), hi_f(sv.x), lo_f(sv.y), hi_f(sv.y)};
+        const float c[4] = {lo_f(in.c.x), hi_f(in.c.x), lo_f(in.c.y), hi_f(in.c.y)};
+        const float sn[4] = {lo_f(in.s.x), hi_f(in.s.x), lo_f(in.s.y), hi_f(in.s.y)};
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const float a = n[2 * p];
@@ -78,6 +101,15 @@ __device__ __forceinline__ uint4 norm_rope_row(uint4 xin, const uint16_t *__rest
     y.z = pack_h2(n[4], n[5]);
     y.w = pack_h2(n[6], n[7]);
     return y;
+}
+
+template <int LANES>
+__device__ __forceinline__ uint4 norm_rope_row(uint4 xin, const uint16_t *__restrict__ w,
+                                               const uint16_t *__restrict__ cos_row,
+                                               const uint16_t *__restrict__ sin_row,
+                                               int half_rot, float eps, int lane) {
+    return norm_rope_apply<LANES>(xin, norm_rope_in<LANES>(w, cos_row, sin_row, half_rot, lane), half_rot, eps,
+                                  lane);
 }
 
 }  // namespace kva

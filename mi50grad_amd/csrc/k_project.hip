@@ -238,6 +238,116 @@ __global__ __launch_bounds__(64 * WAVES) void proj_stream_kernel(ProjectArgs a) 
     proj_reduce_store<NTB, WAVES, RT>(a, acc, red, live, grp, split, wave, lane);
 }
 
+// The x-resident form with the weights staged through LDS: a load
+// instruction that writes LDS directly moves 8 rows x 128 contiguous bytes
+// (two k-steps of one row tile), where a load into MFMA registers can carry
+// only 64 bytes per row (4 lanes of a row x 16 B); each wave then reads its
+// A operands back from its own ring of DEPTH + 1 two-step stages.  No wave
+// reads another's ring, so a wave waits only for its own loads (no
+// barrier).  Stage layout: row r's 16-byte granule g sits at granule
+// g ^ ((r >> 1) & 7), so the 16 rows an A read takes at one granule fall in
+// distinct banks.
+template <int NTB, int WAVES, int RT, int STEPS, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void proj_lds_kernel(ProjectArgs a) {
+    static_assert(STEPS % 2 == 0, "stages of two k-steps");
+    constexpr int SPT = STEPS / 2;       // stages per row tile
+    constexpr int N_ST = RT * SPT;       // stages of a wave
+    constexpr int R = DEPTH + 1;
+    constexpr int kStage = 16 * 128;     // 16 rows x 128 B
+    __shared__ __attribute__((aligned(16))) uint8_t wlds[WAVES][R][kStage];
+    __shared__ float4_t red[WAVES][NTB][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_grp = ((a.n_a + a.n_b) / 16 + RT - 1) / RT;
+    const int grp = blockIdx.x % n_grp;
+    const int split = blockIdx.x / n_grp;
+    const int k0 = (split * WAVES + wave) * STEPS * 32;
+    const int r = lane & 15, g = lane >> 4;
+    const int n_t16 = (a.n_a + a.n_b) / 16;
+    const size_t hidden = static_cast<size_t>(a.hidden);
+    // Row tile i's first row and first element of this wave (uniform), and
+    // whether the tile exists (tiles past the end repeat the last one).
+    const uint16_t *tb[RT];
+    bool live[RT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        const int t16 = grp * RT + i;
+        live[i] = t16 < n_t16;
+        const int row = 16 * min(t16, n_t16 - 1);
+        tb[i] = (row < a.n_a ? a.w_a + static_cast<size_t>(row) * hidden
+                             : a.w_b + static_cast<size_t>(row - a.n_a) * hidden) + k0;
+    }
+    // Load lane mapping: instruction h of a stage covers rows 8h + lane/8;
+    // lane lands at physical granule lane%8, so it fetches logical granule
+    // (lane%8) ^ ((row >> 1) & 7).
+    uint32_t loff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 8 * h + (lane >> 3);
+        const int gl = (lane & 7) ^ ((row >> 1) & 7);
+        loff[h] = (row * static_cast<uint32_t>(a.hidden) + 8 * gl) * 2u;
+    }
+    const uint32_t rbytes = 16u * static_cast<uint32_t>(a.hidden) * 2u;
+    auto issue = [&](int n) {
+        const int i = n / SPT, q = n % SPT;
+        const auto rs = ro_rsrc(tb[i] + 64 * q, rbytes);
+        const uint32_t dst = lds_addr(&wlds[wave][n % R][0]);
+        load_to_lds(rs, dst, loff[0]);
+        load_to_lds(rs, dst + 1024, loff[1]);
+    };
+
+    const auto xr = ro_rsrc(a.x, static_cast<uint32_t>(a.n_tok) * static_cast<uint32_t>(a.hidden) * 2u);
+    uint4 xv[STEPS][NTB];
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j) {
+            const uint32_t off = ((16 * j + r) * static_cast<uint32_t>(a.hidden) + k0 + 8 * g + 32 * st) * 2u;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+            xv[st][j] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    // Take delivery of x before the ring starts: the compiler cannot see the
+    // LDS loads, and a wait for x placed later would drain them.
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j)
+            asm volatile("" : "+v"(xv[st][j].x), "+v"(xv[st][j].y), "+v"(xv[st][j].z), "+v"(xv[st][j].w));
+    float4_t acc[RT][NTB];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < NTB; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int n = 0; n < DEPTH; ++n) issue(n);
+    // A reads: row r at logical granule 4*s + g of a stage's two steps.
+    const int sw = (r >> 1) & 7;
+#pragma unroll
+    for (int n = 0; n < N_ST; ++n) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (n + DEPTH < N_ST) {  // resolved at compile time after unrolling
+            issue(n + DEPTH);
+            wait_vm<2 * DEPTH>();
+        } else {
+            wait_vm<0>();  // the last stages: everything is issued
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t *sb = &wlds[wave][n % R][0] + r * 128;
+        const int i = n / SPT, q = n % SPT;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const uint4 w4 = *reinterpret_cast<const uint4 *>(sb + 16 * ((4 * s2 + g) ^ sw));
+#pragma unroll
+            for (int j = 0; j < NTB; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(w4), as_h8(xv[2 * q + s2][j]), acc[i][j],
+                                                                 0, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    proj_reduce_store<NTB, WAVES, RT>(a, acc, red, live, grp, split, wave, lane);
+}
+
 // Grid: (token, block of 8 head rows) per 256-thread workgroup; one 32-lane
 // group per head row.  Head rows of a token: H query, H gate, Hkv key, Hkv
 // value heads (the order of the weight rows).  The token's metadata and
@@ -256,6 +366,11 @@ __global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
     const int seq = ld_uniform(a.tok_seq + t);
     const int slot = ld_uniform(a.tok_slot + t);
     const int blk = ld_uniform(a.table + static_cast<size_t>(seq) * a.table_stride + (slot >> 4));
+    // The norm weights and cos/sin rows go out with the partials, before
+    // anything waits (gate and value rows load and ignore them).
+    const uint16_t *cos_row = a.cos_tab + static_cast<size_t>(pos) * a.half_rot;
+    const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
+    const NormRopeIn nin = norm_rope_in<32>(hr < H ? a.q_w : a.k_w, cos_row, sin_row, a.half_rot, lane);
     // Every split's partial is loaded at once (splits past a.splits reread
     // split 0 and are not added), then summed in split order.
     const size_t N = static_cast<size_t>(a.n_a) + a.n_b;
@@ -280,10 +395,8 @@ __global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
     y.z = pack_h2(hi[0], hi[1]);
     y.w = pack_h2(hi[2], hi[3]);
 
-    const uint16_t *cos_row = a.cos_tab + static_cast<size_t>(pos) * a.half_rot;
-    const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
     if (hr < H) {
-        const uint4 q = norm_rope_row<32>(y, a.q_w, cos_row, sin_row, a.half_rot, a.eps, lane);
+        const uint4 q = norm_rope_apply<32>(y, nin, a.half_rot, a.eps, lane);
         st16(a.q_out + (static_cast<size_t>(t) * H + hr) * kHeadDim + 8 * lane, q);
         return;
     }
@@ -295,7 +408,7 @@ __global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
     if (a.kv_out) st16(a.kv_out + (static_cast<size_t>(t) * 2 * hkv + kv) * kHeadDim + 8 * lane, y);
     const size_t row_base = (static_cast<size_t>(blk) * kBlockTokens + (slot & 15)) * hkv;
     if (kv < hkv) {
-        const uint4 k = norm_rope_row<32>(y, a.k_w, cos_row, sin_row, a.half_rot, a.eps, lane);
+        const uint4 k = norm_rope_apply<32>(y, nin, a.half_rot, a.eps, lane);
         st16(a.k_pool + (row_base + kv) * kHeadDim + 8 * lane, k);
     } else {
         st16(a.v_pool + (row_base + kv - hkv) * kHeadDim + 8 * lane, y);
@@ -313,8 +426,14 @@ hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
     const int ntb = (a.n_tok + 15) / 16;
     if (ntb <= 2 && a.hidden == kProjStreamSteps * 32 * W * a.splits) {
         constexpr int ST = kProjStreamSteps, SD = kProjStreamDepth;
-        if (ntb == 1) hipLaunchKernelGGL((proj_stream_kernel<1, W, RT, ST, SD>), grid, block, 0, s, a);
-        else hipLaunchKernelGGL((proj_stream_kernel<2, W, RT, ST, SD>), grid, block, 0, s, a);
+        if (kProjLds) {
+            constexpr int LD = kProjLdsDepth;
+            if (ntb == 1) hipLaunchKernelGGL((proj_lds_kernel<1, W, RT, ST, LD>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((proj_lds_kernel<2, W, RT, ST, LD>), grid, block, 0, s, a);
+        } else {
+            if (ntb == 1) hipLaunchKernelGGL((proj_stream_kernel<1, W, RT, ST, SD>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((proj_stream_kernel<2, W, RT, ST, SD>), grid, block, 0, s, a);
+        }
     } else switch (ntb) {
         case 1: hipLaunchKernelGGL((proj_gemm_kernel<1, W, P, RT>), grid, block, 0, s, a); break;
         case 2: hipLaunchKernelGGL((proj_gemm_kernel<2, W, P, RT>), grid, block, 0, s, a); break;

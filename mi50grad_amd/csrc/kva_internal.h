@@ -54,6 +54,8 @@ constexpr int kProjHiddenQuantum = 512;  // hidden must be a multiple of this
 constexpr int kProjWgPerCu = 1;     // GEMM workgroups per CU the split aims for, at most
 constexpr int kProjStreamSteps = 10;  // k-steps per wave of the x-resident form (up to 32 tokens)
 constexpr int kProjStreamDepth = 8;   // weight loads in flight per wave there
+constexpr bool kProjLds = true;       // stage the weights through LDS in that form
+constexpr int kProjLdsDepth = 6;      // two-step stages in flight per wave there
 struct ProjectArgs {
     const uint16_t *x;        // [n_tok][hidden], this chunk's first token
     const uint16_t *w_a;
