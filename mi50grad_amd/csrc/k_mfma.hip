@@ -14,9 +14,11 @@
 // row — every head of the group attends to the same K/V — so four waves of
 // 16 x NT rows each (Q = 64*NT/G) leave at most G-1 rows idle (the tree
 // verify's 9 nodes x 6 heads fill 54 of 64 rows).  Work is split stream-K
-// over 32-key blocks: the blocks of all units are laid end to end and each
-// workgroup takes an equal share; units cut by a share boundary leave
-// partials for mq_combine_kernel.
+// over 32-key blocks: the blocks of all units are laid end to end, head-major
+// (kv head, sequence, tile), and each workgroup takes an equal share, the
+// shares dealt out XCD by XCD so the tiles of one (sequence, head) run on
+// one XCD and their repeated reads of its keys come from that XCD's L2;
+// units cut by a share boundary leave partials for mq_combine_kernel.
 //
 // K/V blocks travel HBM -> LDS by buffer loads that write LDS directly (no
 // register staging), through a ring of four 32 KB stages: while block i is
@@ -89,16 +91,22 @@ struct Unit {
     const int32_t *trow;  // block-table row
 };
 
+// Units are head-major: unit u is tile r = u % U1 of head u / U1 (U1 =
+// upre[n_seqs], one head's units), and sequence b holds tiles
+// [upre[b], upre[b+1]).  b is a hint (a sequence at or before the unit's
+// within the same head), so a walk in unit order scans each sequence once.
 __device__ __forceinline__ Unit load_unit(const MultiQueryArgs &a, int u, int b) {
     Unit x;
     x.u = u;
     x.ub = ld_uniform(a.mq_pre + u) + kMqUnitCost;  // its first block (positions before: the start cost)
     x.ue = ld_uniform(a.mq_pre + u + 1);
-    while (ld_uniform(a.upre + b + 1) <= u) ++b;  // units are in sequence order
+    const int U1 = ld_uniform(a.upre + a.n_seqs);
+    x.h = u / U1;
+    const int r = u - x.h * U1;
+    if (r < ld_uniform(a.upre + b)) b = 0;  // the walk entered the next head
+    while (ld_uniform(a.upre + b + 1) <= r) ++b;
     x.b = b;
-    const int r = u - ld_uniform(a.upre + b);
-    x.tile = r / a.num_kv_heads;
-    x.h = r - x.tile * a.num_kv_heads;
+    x.tile = r - ld_uniform(a.upre + b);
     x.ctx = ld_uniform(a.ctx_lens + b);
     x.ns = ld_uniform(a.new_start + b);
     x.tok = ld_uniform(a.tok_off + b);
@@ -156,10 +164,19 @@ __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(ha
 // only on such jumps, not at every block where some row's max grew.
 constexpr float kRescaleSlack = 8.0f;
 
+// Stream-K share of workgroup i.  Workgroup i runs on XCD i % 8, so with
+// W a multiple of 8 the shares are dealt out XCD by XCD: XCD x takes shares
+// [x*W/8, (x+1)*W/8), consecutive in unit order.  With head-major units the
+// tiles of one (sequence, head), which all read that head's keys, then run
+// together on one XCD and share its L2.
+__device__ __forceinline__ int mq_share_of(int i, int W) {
+    return (W & 7) == 0 ? (i & 7) * (W >> 3) + (i >> 3) : i;
+}
+
 template <int NT, int WAVES, bool TREE>
 __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t ring[kRing][2 * kTileBytes];
-    const int w = blockIdx.x;
+    const int w = mq_share_of(blockIdx.x, a.n_wg);  // this workgroup's share (and partial slots)
     const int W = a.n_wg;
     const int NB = a.total_blocks;
     const int q0 = mq_wg_start(w, NB, W);
@@ -188,7 +205,8 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
     // Issue side: the unit and block of the next load, kRing-1 blocks ahead
     // of the compute side, across unit boundaries.
     const int u0 = upper_index(a.mq_pre, a.n_units, q0);
-    Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0));
+    const int U1 = ld_uniform(a.upre + a.n_seqs);
+    Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0 % U1));
     int ig = max(q0, iu.ub);
     if (ig >= q1) return;  // the share holds only a unit's start cost
     int ipage = 0;  // page of the next issue
@@ -431,11 +449,15 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int lane = threadIdx.x & 63;
     const int ub = a.mq_pre[u] + kMqUnitCost;  // the unit's first block
     const int ue = a.mq_pre[u + 1];
-    // Sequence of unit u: the number of sequences whose units end at or before u.
+    // Head and tile index of unit u (head-major units), and its sequence:
+    // the number of sequences whose tiles end at or before the tile.
+    const int U1 = a.upre[a.n_seqs];
+    const int h = u / U1;
+    const int r = u - h * U1;
     int b = 0;
     for (int c0 = 0; c0 < a.n_seqs; c0 += 64) {
         const int i = c0 + lane;
-        const uint64_t m = __ballot(i < a.n_seqs && a.upre[i + 1] <= u);
+        const uint64_t m = __ballot(i < a.n_seqs && a.upre[i + 1] <= r);
         b += __popcll(m);
         if (m != ~0ull) break;
     }
@@ -449,9 +471,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int hkv = a.num_kv_heads;
     const int G = a.num_heads / hkv;
     const int Q = a.q_tile;
-    const int x = u - a.upre[b];
-    const int tile = x / hkv;
-    const int h = x - tile * hkv;
+    const int tile = r - a.upre[b];
     const int rho = 16 * blockIdx.y + (threadIdx.x >> 4);
     const int d0 = (threadIdx.x & 15) * 16;
     const int iq = rho / G;

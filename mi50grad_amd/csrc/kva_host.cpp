@@ -682,24 +682,32 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     }
     p_off[n_seqs] = t;
     p_pre[n_seqs] = static_cast<int32_t>(pages);
-    // Multi-query units in (sequence, tile, kv head) order with their key
+    // Multi-query units in (kv head, sequence, tile) order with their key
     // blocks: a tree tile reads the whole cache, a causal tile reads up to
-    // its last token's slot.
+    // its last token's slot.  upre[b] counts the tiles of earlier sequences
+    // (one head's units); unit u is head u / upre[n_seqs].  Head-major order
+    // puts all tiles of one (sequence, head) in consecutive stream-K shares,
+    // which the kernel places on one XCD, so the tiles' repeated reads of
+    // that head's keys hit the XCD's L2.
     int32_t *p_upre = at<int32_t>(h, o_upre), *p_mqpre = at<int32_t>(h, o_mqpre);
-    int64_t units = 0, blocks = 0;
+    int64_t tiles_all = 0;
     for (int32_t b = 0; b < n_seqs; ++b) {
-        p_upre[b] = static_cast<int32_t>(units);
-        const int32_t tiles = (n_new[b] + mq_q - 1) / mq_q;
-        for (int32_t tl = 0; tl < tiles; ++tl) {
-            const int64_t keys = tree_bits ? p_ctx[b] : p_start[b] + std::min(n_new[b], (tl + 1) * mq_q);
-            const int64_t nb = (keys + kva::kMqKeys - 1) / kva::kMqKeys;
-            for (int32_t hh = 0; hh < c->cfg.num_kv_heads; ++hh) {
+        p_upre[b] = static_cast<int32_t>(tiles_all);
+        tiles_all += (n_new[b] + mq_q - 1) / mq_q;
+    }
+    p_upre[n_seqs] = static_cast<int32_t>(tiles_all);
+    int64_t units = 0, blocks = 0;
+    for (int32_t hh = 0; hh < c->cfg.num_kv_heads; ++hh) {
+        for (int32_t b = 0; b < n_seqs; ++b) {
+            const int32_t tiles = (n_new[b] + mq_q - 1) / mq_q;
+            for (int32_t tl = 0; tl < tiles; ++tl) {
+                const int64_t keys = tree_bits ? p_ctx[b] : p_start[b] + std::min(n_new[b], (tl + 1) * mq_q);
+                const int64_t nb = (keys + kva::kMqKeys - 1) / kva::kMqKeys;
                 p_mqpre[units++] = static_cast<int32_t>(blocks);
                 blocks += kva::kMqUnitCost + nb;
             }
         }
     }
-    p_upre[n_seqs] = static_cast<int32_t>(units);
     p_mqpre[units] = static_cast<int32_t>(blocks);
     if (tree_bits) std::memcpy(h + o_bits, tree_bits, sizeof(uint64_t) * n_tok);
 

@@ -172,10 +172,10 @@ struct MultiQueryArgs {
     const int32_t *new_start; // device [n_seqs]: first new slot
     const int32_t *tok_off;   // device [n_seqs+1]: new-token ranges
     const uint64_t *tok_bits; // device [T] (tree mode) or null
-    const int32_t *upre;      // device [n_seqs+1]: units of earlier sequences
+    const int32_t *upre;      // device [n_seqs+1]: tiles of earlier sequences (units of one head)
     const int32_t *mq_pre;    // device [n_units+1]: positions of earlier units (blocks + kMqUnitCost each)
     int32_t n_seqs;
-    int32_t n_units;          // (sequence, 16-token tile, kv head) units
+    int32_t n_units;          // (kv head, sequence, token tile) units, head-major
     int32_t total_blocks;     // positions of all units (blocks + kMqUnitCost each)
     int32_t n_wg;             // workgroups sharing the blocks (stream-K)
     int32_t num_heads;
