@@ -111,3 +111,68 @@ def test_graph_replay_matches_eager(device, lengths, split):
     stream.destroy()
     eager.destroy()
     graphed.destroy()
+
+
+def test_graph_replay_project_append(device):
+    """The producer path recorded too: per layer kva_project_append (fused
+    projection + norm + RoPE + append) then the gated decode, one step
+    recorded and replayed with fresh hidden states; every replay equals the
+    eager twin bit for bit, and so do the pools at the end."""
+    say("graph replay of project_append + gated decode")
+    rng = np.random.default_rng(8)
+    lengths, hidden = [30, 47, 3], 512
+    eager, graphed = _twin(lengths, 0, seed=12)
+    B = len(lengths)
+    tables = Tables(device, 512)
+    stream = Stream()
+
+    def f16(shape, s=1.0):
+        return (rng.standard_normal(shape, dtype=np.float32) * s).astype(np.float16)
+
+    w = [dict(wq=device.array(f16((2 * H * D, hidden), hidden ** -0.5)),
+              wkv=device.array(f16((2 * HKV * D, hidden), hidden ** -0.5)),
+              qw=device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)),
+              kw=device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16))) for _ in range(LAYERS)]
+    bufs = [[dict(x=device.empty((B, hidden), np.float16), q=device.empty((B, H, D), np.float16),
+                  g=device.empty((B, H, D), np.float16), out=device.empty((B, H, D), np.float16))
+             for _ in range(LAYERS)] for _ in range(2)]
+
+    def calls(cache, which, stream_h):
+        for layer in range(LAYERS):
+            b, p = bufs[which][layer], w[layer]
+            cache.project_append(layer, b["x"], hidden, p["wq"], p["wkv"], p["qw"], p["kw"], tables.d_cos,
+                                 tables.d_sin, tables.rows, b["q"], b["g"], stream=stream_h)
+            cache.decode(layer, b["q"], b["out"], stream=stream_h, gate=b["g"])
+
+    graph = None
+    for step in range(12):
+        xs = [f16((B, hidden)) for _ in range(LAYERS)]
+        for which in range(2):
+            for layer in range(LAYERS):
+                device.upload(bufs[which][layer]["x"].ptr, xs[layer].tobytes())
+        device.synchronize()
+        eager.begin_step(list(range(B)), [1] * B)
+        calls(eager, 0, None)
+        graphed.begin_step(list(range(B)), [1] * B, stream=stream.handle)
+        if graph is None:
+            graph = graphed.record_step(stream.handle)
+            calls(graphed, 1, stream.handle)
+            graph.end()
+        graph.launch()
+        stream.synchronize()
+        device.synchronize()
+        for layer in range(LAYERS):
+            for name in ("q", "g", "out"):
+                got = bufs[1][layer][name].numpy().view(np.uint16)
+                exp = bufs[0][layer][name].numpy().view(np.uint16)
+                assert np.array_equal(got, exp), (step, layer, name)
+    for layer in range(LAYERS):
+        ke, ve = eager.download_pools(layer)
+        kg, vg = graphed.download_pools(layer)
+        assert np.array_equal(ke.view(np.uint16), kg.view(np.uint16))
+        assert np.array_equal(ve.view(np.uint16), vg.view(np.uint16))
+    graph.destroy()
+    stream.synchronize()
+    stream.destroy()
+    eager.destroy()
+    graphed.destroy()
