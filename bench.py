@@ -18,7 +18,9 @@ over its average duration from HIP events recorded on the launch stream
 around each decode launch inside the timed region.  ``cpu_baseline`` is the
 numpy oracle on a bounded sample of the same workload on this host.
 
-Other workloads: --workload ctx8192 (every sequence at 8192 rows), c2
+Other workloads: --workload c1 (the one-layer config-1 step: GPU latency
+next to the numpy oracle's, 1 and all BLAS threads), ctx8192 (every
+sequence at 8192 rows), c2
 (16 layers, B=1, 128 decode steps growing 128 -> 256 rows), c2graph (the
 same with the 16-layer step recorded once and replayed), c4 (chunked
 prefill), c5 (tree verify + rollback), proj (config 3 with its producer:
@@ -218,6 +220,84 @@ def proj_workload(dev, steps, warmup, hidden=5120):
     return {"wall_s": wall, "steps": steps, "B": B, "hidden": hidden, "alg_bytes_proj": alg,
             "weight_bytes": nq + nkv, "proj_avg_us": float(np.mean(proj_ms) * 1e3),
             "decode_avg_us": float(np.mean(dec_ms) * 1e3)}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def c1_workload(dev, reps=200):
+    """Config 1: one layer, batch 1, 255 cached rows; append at position 255
+    (norm + RoPE of q and k, K/V into the cache) then decode over 256 rows.
+    GPU: HIP events around append + decode, median of `reps` calls.  CPU: the
+    numpy oracle's same step (norm + RoPE of the 28 rows, then decode
+    attention), median of 25 calls with 1 BLAS thread and with all of them."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import kvattn_oracle as orc
+
+    x = wl.c1_inputs(0)
+    cache = PagedKVCache(n_layers=1, max_seqs=1, max_blocks=16, max_blocks_per_seq=16, max_step_tokens=16)
+    cache.reserve(0, 256)
+    cache.sync_tables()
+    ids = cache.blocks(0)
+    kimg = np.zeros((16, 16, HKV, D), np.float16)
+    vimg = np.zeros_like(kimg)
+    for r in range(255):
+        kimg[ids[r // 16], r % 16] = x.k_cache[r]
+        vimg[ids[r // 16], r % 16] = x.v_cache[r]
+    kp, vp = cache.layer_pools(0)
+    dev.upload(kp, kimg.tobytes())
+    dev.upload(vp, vimg.tobytes())
+    cos, sin = rope_tables(256)
+    d_cos, d_sin = dev.array(cos), dev.array(sin)
+    qw, kw = dev.array(x.q_norm), dev.array(x.k_norm)
+    q, k, v = dev.empty((1, H, D), np.float16), dev.array(x.k_new), dev.array(x.v_new)
+    out = dev.empty((1, H, D), np.float16)
+    ms = []
+    for i in range(reps + 10):
+        cache.set_len(0, 255)
+        cache.begin_step([0], [1])
+        dev.upload(q.ptr, x.q.tobytes())
+        a, b = Event(), Event()
+        a.record()
+        cache.append(0, q, k, v, qw, kw, d_cos, d_sin, 256)
+        cache.decode(0, q, out)
+        b.record()
+        b.synchronize()
+        if i >= 10:
+            ms.append(a.elapsed_ms(b))
+        a.destroy()
+        b.destroy()
+    cache.destroy()
+
+    pos = np.array([255])
+
+    def cpu_step():
+        qn = orc.qknorm_rope_exact(x.q.reshape(H, D), x.q_norm, np.repeat(cos[pos], H, 0), np.repeat(sin[pos], H, 0))
+        kn = orc.qknorm_rope_exact(x.k_new.reshape(HKV, D), x.k_norm, np.repeat(cos[pos], HKV, 0),
+                                   np.repeat(sin[pos], HKV, 0))
+        kc = np.concatenate([x.k_cache, kn.reshape(1, HKV, D)])
+        vc = np.concatenate([x.v_cache, x.v_new])
+        return orc.decode_attention(qn.reshape(1, H, D), [kc], [vc])
+
+    cpu = {}
+    for label, n in (("1", 1), ("all", None)):
+        with threadpool_limits(n):
+            ts = []
+            for _ in range(25):
+                t0 = time.perf_counter()
+                cpu_step()
+                ts.append(time.perf_counter() - t0)
+        cpu[label] = float(np.median(ts) * 1e6)
+    return {"gpu_us": float(np.median(ms) * 1e3), "gpu_min_us": float(np.min(ms) * 1e3), "cpu_us_1": cpu["1"],
+            "cpu_us_all": cpu["all"], "reps": reps}
 
 
 def c2_workload(dev, steps_unused, warmup, graph=False, split=0):
@@ -459,7 +539,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "copy"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "copy"])
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -474,6 +554,21 @@ def main() -> int:
         print(json.dumps({"metric": "HBM stream copy GB/s", "value": r["gbs"], "unit": "GB/s",
                           "n_gpus": 1, "avg_us": r["avg_us"], "bytes_per_launch": r["bytes_per_launch"],
                           "higher_is_better": True}))
+        return 0
+    if args.workload == "c1":
+        r = c1_workload(dev)
+        by = 256 * ROW_BYTES + 2 * H * D * 2 + 2 * HKV * D * 2
+        print(json.dumps({
+            "metric": "config-1 one-layer step latency (append at 255 + decode over 256, B=1)",
+            "value": r["gpu_us"], "unit": "us", "n_gpus": 1, "steps": r["reps"], "higher_is_better": False,
+            "dtype": "f16", "data": "synthetic (seed 0, the config-1 recipe)",
+            "config": {"workload": "C1", "layers": 1, "rows": 256},
+            "gpu_min_us": r["gpu_min_us"], "alg_bytes": by, "gpu_gbs": by / (r["gpu_us"] * 1e-6) / 1e9,
+            "cpu_baseline": {"value": r["cpu_us_1"], "unit": "us", "cores": 1, "kind": "port",
+                             "all_threads_us": r["cpu_us_all"], "host_logical_cpus": os.cpu_count(),
+                             "cpu_model": _cpu_model(),
+                             "sample": "the whole config-1 step in the numpy oracle, median of 25 calls, "
+                                       "1 BLAS thread (value) and all BLAS threads"}}))
         return 0
     if args.workload in ("c2", "c2graph"):
         graph = args.workload == "c2graph"

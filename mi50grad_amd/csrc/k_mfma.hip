@@ -561,7 +561,6 @@ hipError_t launch_multi_query(const MultiQueryArgs &a, hipStream_t s) {
     if (G < 1 || G > kMqMaxGroup || a.num_heads % a.num_kv_heads) return hipErrorInvalidValue;
     if (a.q_tile != mq_tile_tokens(G, a.n_waves, a.n_t)) return hipErrorInvalidValue;
     if (a.n_t == 1 && a.n_waves == 4) return launch_mq<1, 4>(a, s);
-    if (a.n_t == 2 && a.n_waves == 4) return launch_mq<2, 4>(a, s);
     if (a.n_t == 1 && a.n_waves == 8) return launch_mq<1, 8>(a, s);
     return hipErrorInvalidValue;
 }

@@ -20,7 +20,8 @@
 //   weights against zero x instead of branching, so the compiler's
 //   load-counter waits never drain the loads in flight.  The waves' sums
 //   meet in LDS in a fixed order and go out as fp32 partials
-//   [split][token][row].
+//   [split][token][row].  proj_lds_kernel, the form for up to 32 tokens,
+//   keeps x in registers and stages the weights through LDS instead.
 // proj_finish_kernel: per (token, head), one 32-lane group sums the splits
 //   in order, rounds to fp16 and then does what the append kernel does:
 //   Q -> norm + RoPE -> q_out, Q_gate -> gate_out, K -> norm + RoPE -> its
@@ -178,67 +179,7 @@ __global__ __launch_bounds__(64 * WAVES) void proj_gemm_kernel(ProjectArgs a) {
 
 // The form for up to 32 tokens and STEPS k-steps per wave: each wave's x
 // slice stays in registers for the whole kernel (loaded once at the start)
-// and the weights stream one row tile at a time, DEPTH loads along k ahead
-// of the MFMAs, so the loads in flight cover a few rows far along k
-// (contiguous bytes per row) rather than many rows one step deep.  The loop
-// over (row tile, k-step) is fully unrolled: every ring slot keeps a fixed
-// register.
-template <int NTB, int WAVES, int RT, int STEPS, int DEPTH>
-__global__ __launch_bounds__(64 * WAVES) void proj_stream_kernel(ProjectArgs a) {
-    constexpr int N_LD = RT * STEPS;   // weight loads of a wave
-    constexpr int R = DEPTH + 1;
-    __shared__ float4_t red[WAVES][NTB][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n_grp = ((a.n_a + a.n_b) / 16 + RT - 1) / RT;
-    const int grp = blockIdx.x % n_grp;
-    const int split = blockIdx.x / n_grp;
-    const int k0 = (split * WAVES + wave) * STEPS * 32;
-    const int r = lane & 15, g = lane >> 4;
-    const uint16_t *wt[RT];
-    bool live[RT];
-    proj_tiles<RT>(a, grp, r * a.hidden + k0 + 8 * g, wt, live);
-    const auto xr = ro_rsrc(a.x, static_cast<uint32_t>(a.n_tok) * static_cast<uint32_t>(a.hidden) * 2u);
-
-    uint4 xv[STEPS][NTB];
-#pragma unroll
-    for (int st = 0; st < STEPS; ++st)
-#pragma unroll
-        for (int j = 0; j < NTB; ++j) {
-            const uint32_t off = ((16 * j + r) * static_cast<uint32_t>(a.hidden) + k0 + 8 * g + 32 * st) * 2u;
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
-            xv[st][j] = make_uint4(v[0], v[1], v[2], v[3]);
-        }
-    float4_t acc[RT][NTB];
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int j = 0; j < NTB; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-    uint4 ring[R];
-#pragma unroll
-    for (int n = 0; n < DEPTH; ++n) {
-        __builtin_amdgcn_sched_barrier(0);
-        ring[n] = ld16(wt[n / STEPS] + 32 * (n % STEPS));
-    }
-#pragma unroll
-    for (int n = 0; n < N_LD; ++n) {
-        __builtin_amdgcn_sched_barrier(0);
-        if (n + DEPTH < N_LD) {  // resolved at compile time after unrolling
-            const int m = n + DEPTH;
-            ring[m % R] = ld16(wt[m / STEPS] + 32 * (m % STEPS));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const int i = n / STEPS, st = n % STEPS;
-#pragma unroll
-        for (int j = 0; j < NTB; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(ring[n % R]), as_h8(xv[st][j]), acc[i][j], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    proj_reduce_store<NTB, WAVES, RT>(a, acc, red, live, grp, split, wave, lane);
-}
-
-// The x-resident form with the weights staged through LDS: a load
+// and the weights stream one row tile at a time through LDS: a load
 // instruction that writes LDS directly moves 8 rows x 128 contiguous bytes
 // (two k-steps of one row tile), where a load into MFMA registers can carry
 // only 64 bytes per row (4 lanes of a row x 16 B); each wave then reads its
@@ -425,15 +366,9 @@ hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
     const dim3 block(64 * W);
     const int ntb = (a.n_tok + 15) / 16;
     if (ntb <= 2 && a.hidden == kProjStreamSteps * 32 * W * a.splits) {
-        constexpr int ST = kProjStreamSteps, SD = kProjStreamDepth;
-        if (kProjLds) {
-            constexpr int LD = kProjLdsDepth;
-            if (ntb == 1) hipLaunchKernelGGL((proj_lds_kernel<1, W, RT, ST, LD>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((proj_lds_kernel<2, W, RT, ST, LD>), grid, block, 0, s, a);
-        } else {
-            if (ntb == 1) hipLaunchKernelGGL((proj_stream_kernel<1, W, RT, ST, SD>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((proj_stream_kernel<2, W, RT, ST, SD>), grid, block, 0, s, a);
-        }
+        constexpr int ST = kProjStreamSteps, LD = kProjLdsDepth;
+        if (ntb == 1) hipLaunchKernelGGL((proj_lds_kernel<1, W, RT, ST, LD>), grid, block, 0, s, a);
+        else hipLaunchKernelGGL((proj_lds_kernel<2, W, RT, ST, LD>), grid, block, 0, s, a);
     } else switch (ntb) {
         case 1: hipLaunchKernelGGL((proj_gemm_kernel<1, W, P, RT>), grid, block, 0, s, a); break;
         case 2: hipLaunchKernelGGL((proj_gemm_kernel<2, W, P, RT>), grid, block, 0, s, a); break;

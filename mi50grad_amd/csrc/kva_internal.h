@@ -53,9 +53,7 @@ constexpr int kProjDepth = 1;       // k-steps of loads in flight per wave (gene
 constexpr int kProjHiddenQuantum = 512;  // hidden must be a multiple of this
 constexpr int kProjWgPerCu = 1;     // GEMM workgroups per CU the split aims for, at most
 constexpr int kProjStreamSteps = 10;  // k-steps per wave of the x-resident form (up to 32 tokens)
-constexpr int kProjStreamDepth = 8;   // weight loads in flight per wave there
-constexpr bool kProjLds = true;       // stage the weights through LDS in that form
-constexpr int kProjLdsDepth = 6;      // two-step stages in flight per wave there
+constexpr int kProjLdsDepth = 6;      // two-step LDS stages in flight per wave there
 struct ProjectArgs {
     const uint16_t *x;        // [n_tok][hidden], this chunk's first token
     const uint16_t *w_a;
@@ -182,7 +180,7 @@ struct MultiQueryArgs {
     int32_t num_kv_heads;
     int32_t tree;             // 0 = causal chunk, 1 = tree mask
     int32_t n_waves;          // waves per workgroup (4 or 8)
-    int32_t n_t;              // 16-row MFMA tiles per wave (1 or 2)
+    int32_t n_t;              // 16-row MFMA tiles per wave (1: the form launched)
     int32_t q_tile;           // new tokens per unit tile: mq_tile_tokens(G, n_waves, n_t)
     float *ws_acc;            // [2*n_wg][kMqSlotRows][256] partial slots
     float *ws_ml;             // [2*n_wg][kMqSlotRows][2]
