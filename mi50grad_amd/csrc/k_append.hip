@@ -13,38 +13,39 @@ namespace kva {
 namespace {
 
 // One 32-lane group per row; rows of a token: H query heads, Hkv key heads,
-// Hkv value heads.  8 rows per 256-thread workgroup.
+// Hkv value heads.  8 rows per 256-thread workgroup, all of one token (the
+// launch packs each token's rows into whole workgroups), so the token's
+// position, sequence, slot and page id are workgroup-uniform scalar loads,
+// and the norm weights and cos/sin rows go out with the row's own load.
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     const int rows_per_tok = a.num_heads + 2 * a.num_kv_heads;
-    const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int blocks_per_tok = (rows_per_tok + 7) / 8;
+    const int t = blockIdx.x / blocks_per_tok;
+    const int hr = (blockIdx.x - t * blocks_per_tok) * 8 + (threadIdx.x >> 5);
     const int lane = threadIdx.x & 31;
-    if (row >= a.n_tok * rows_per_tok) return;  // whole 32-lane group leaves
-    const int t = row / rows_per_tok;
-    const int hr = row - t * rows_per_tok;
+    if (hr >= rows_per_tok) return;  // whole 32-lane group leaves
     const int hkv = a.num_kv_heads;
+    const int pos = ld_uniform(a.tok_pos + t);
+    const uint16_t *cos_row = a.cos_tab + static_cast<size_t>(pos) * a.half_rot;
+    const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
 
     if (hr < a.num_heads) {
         uint16_t *x = a.q + (static_cast<size_t>(t) * a.num_heads + hr) * kHeadDim;
-        const int pos = a.tok_pos[t];
-        const uint4 y = norm_rope_row<32>(ld16(x + 8 * lane), a.q_w,
-                                          a.cos_tab + static_cast<size_t>(pos) * a.half_rot,
-                                          a.sin_tab + static_cast<size_t>(pos) * a.half_rot,
-                                          a.half_rot, a.eps, lane);
-        st16(x + 8 * lane, y);
+        const uint4 xin = ld16(x + 8 * lane);
+        const NormRopeIn nin = norm_rope_in<32>(a.q_w, cos_row, sin_row, a.half_rot, lane);
+        st16(x + 8 * lane, norm_rope_apply<32>(xin, nin, a.half_rot, a.eps, lane));
         return;
     }
-    const int seq = a.tok_seq[t];
-    const int slot = a.tok_slot[t];
-    const int blk = a.table[static_cast<size_t>(seq) * a.table_stride + (slot >> 4)];
+    const int seq = ld_uniform(a.tok_seq + t);
+    const int slot = ld_uniform(a.tok_slot + t);
+    const int blk = ld_uniform(a.table + static_cast<size_t>(seq) * a.table_stride + (slot >> 4));
     const size_t row_base = (static_cast<size_t>(blk) * kBlockTokens + (slot & 15)) * hkv;
     if (hr < a.num_heads + hkv) {
         const int kh = hr - a.num_heads;
         uint16_t *x = a.k + (static_cast<size_t>(t) * hkv + kh) * kHeadDim;
-        const int pos = a.tok_pos[t];
-        const uint4 y = norm_rope_row<32>(ld16(x + 8 * lane), a.k_w,
-                                          a.cos_tab + static_cast<size_t>(pos) * a.half_rot,
-                                          a.sin_tab + static_cast<size_t>(pos) * a.half_rot,
-                                          a.half_rot, a.eps, lane);
+        const uint4 xin = ld16(x + 8 * lane);
+        const NormRopeIn nin = norm_rope_in<32>(a.k_w, cos_row, sin_row, a.half_rot, lane);
+        const uint4 y = norm_rope_apply<32>(xin, nin, a.half_rot, a.eps, lane);
         st16(x + 8 * lane, y);
         st16(a.k_pool + (row_base + kh) * kHeadDim + 8 * lane, y);
     } else {
@@ -71,9 +72,9 @@ __global__ __launch_bounds__(256) void legacy_norm_kernel(LegacyNormArgs a) {
 }  // namespace
 
 hipError_t launch_append(const AppendArgs &a, hipStream_t s) {
-    const int rows = a.n_tok * (a.num_heads + 2 * a.num_kv_heads);
-    if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(append_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, a);
+    if (a.n_tok <= 0) return hipSuccess;
+    const int blocks_per_tok = (a.num_heads + 2 * a.num_kv_heads + 7) / 8;
+    hipLaunchKernelGGL(append_kernel, dim3(a.n_tok * blocks_per_tok), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
