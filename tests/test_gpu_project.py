@@ -196,3 +196,37 @@ def test_project_optional_outputs_and_errors(device):
     assert np.array_equal(q_out.numpy().view(np.uint16), q.view(np.uint16))
     _check_cache_rows(cache, kr, vr, lengths, [1, 1], k, v)
     cache.destroy()
+
+
+def test_project_other_head_shape(device):
+    """8 query and 2 kv heads (G = 4): 5120 weight rows, so the last group
+    of 7 row tiles is partial (its missing tiles are loaded, never
+    written); every output still bit-exact on fp32-exact inputs."""
+    rng = np.random.default_rng(35)
+    h, hkv, hidden = 8, 2, 1024
+    lengths, n_new = [19, 250, 64], [2, 1, 5]
+    T = sum(n_new)
+    ids = _ids(rng, [(L + n + 15) // 16 for L, n in zip(lengths, n_new)])
+    say("project_append with 8 q / 2 kv heads")
+    cache, kr, vr = build_cache(lengths, ids, extra_rows=n_new, num_heads=h, num_kv_heads=hkv, rng=rng)
+    tables = Tables(device, 512)
+    wq = (rng.integers(-2, 3, (2 * h * D, hidden), dtype=np.int8) * 2.0 ** -7).astype(np.float16)
+    wkv = (rng.integers(-2, 3, (2 * hkv * D, hidden), dtype=np.int8) * 2.0 ** -7).astype(np.float16)
+    qw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    kw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    x = rng.integers(-3, 4, (T, hidden), dtype=np.int8).astype(np.float16)
+    pos = [L + i for L, n in zip(lengths, n_new) for i in range(n)]
+    cache.begin_step(list(range(3)), n_new)
+    q_out, g_out = device.empty((T, h, D), np.float16), device.empty((T, h, D), np.float16)
+    kv_out = device.empty((T, 2, hkv, D), np.float16)
+    cache.project_append(0, device.array(x), hidden, device.array(wq), device.array(wkv), device.array(qw),
+                         device.array(kw), tables.d_cos, tables.d_sin, tables.rows, q_out, g_out, kv_out)
+    device.synchronize()
+    q, gate, k_raw, k, v = orc.project_append(x, wq, wkv, qw, kw, tables.cos[pos], tables.sin[pos], h, hkv)
+    assert np.array_equal(q_out.numpy().view(np.uint16), q.view(np.uint16))
+    assert np.array_equal(g_out.numpy().view(np.uint16), gate.view(np.uint16))
+    kvo = kv_out.numpy()
+    assert np.array_equal(kvo[:, 0].view(np.uint16), k_raw.view(np.uint16))
+    assert np.array_equal(kvo[:, 1].view(np.uint16), v.view(np.uint16))
+    _check_cache_rows(cache, kr, vr, lengths, n_new, k, v)
+    cache.destroy()
