@@ -524,6 +524,60 @@ def cpu_baseline(budget_s: float = 10.0):
                       f"host {os.cpu_count()} logical CPUs"}
 
 
+def _median_cpu(fn, budget_s: float, threads):
+    """Median time of fn() (3 warm-ups, then until ~budget_s or 20 calls,
+    at least 5) under a BLAS thread limit (None = all)."""
+    from threadpoolctl import threadpool_limits
+
+    ts = []
+    with threadpool_limits(threads):
+        for _ in range(3):
+            fn()
+        t_end = time.perf_counter() + budget_s
+        while len(ts) < 5 or (len(ts) < 20 and time.perf_counter() < t_end):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts)
+
+
+def cpu_baseline_c4(budget_s: float = 8.0):
+    """The numpy oracle's causal chunk attention for one config-4 sequence
+    (P = 256: a 512-token chunk over 768 keys), one layer, 1 BLAS thread;
+    reported as TFLOP/s on the unmasked pairs, as the GPU row."""
+    from oracle import kvattn_oracle as orc
+
+    rng = np.random.default_rng(4)
+    P, C = 256, wl.C4_CHUNK
+    q = wl.normal_f16(rng, (C, H, D))
+    k = wl.normal_f16(rng, (P + C, HKV, D))
+    v = wl.normal_f16(rng, (P + C, HKV, D))
+    t, n = _median_cpu(lambda: orc.chunk_attention(q, k, v, P), budget_s, 1)
+    flops = 4 * H * D * sum(P + i + 1 for i in range(C))
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle chunk_attention, one config-4 sequence (P={P}, chunk {C}), one layer, "
+                      f"median of {n} calls, 1 BLAS thread; host {os.cpu_count()} logical CPUs ({_cpu_model()})"}
+
+
+def cpu_baseline_c5(budget_s: float = 8.0):
+    """The numpy oracle's tree attention for one config-5 sequence (its
+    first: the 9-node tree over the cached rows), one layer, 1 BLAS thread;
+    reported as KV GB/s with the GPU row's byte count."""
+    from oracle import kvattn_oracle as orc
+
+    spec = wl.c5_spec(0)
+    L = int(spec.lengths[0])
+    rng = np.random.default_rng(5)
+    q = wl.normal_f16(rng, (9, H, D))
+    kc, vc = wl.normal_f16(rng, (L, HKV, D)), wl.normal_f16(rng, (L, HKV, D))
+    kt, vt = wl.normal_f16(rng, (9, HKV, D)), wl.normal_f16(rng, (9, HKV, D))
+    t, n = _median_cpu(lambda: orc.tree_attention(q, kc, vc, kt, vt, wl.C5_PARENTS), budget_s, 1)
+    by = L * ROW_BYTES + 9 * ROW_BYTES + 2 * 9 * H * D * 2
+    return {"value": by / t / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle tree_attention, config-5 sequence 0 (ctx {L}, 9-node tree), one layer, "
+                      f"median of {n} calls, 1 BLAS thread; host {os.cpu_count()} logical CPUs ({_cpu_model()})"}
+
+
 def load_traffic(name: str):
     p = ROOT / "profiles" / name
     if not p.exists():
@@ -603,7 +657,8 @@ def main() -> int:
         r = c4_workload(dev, args.steps, args.warmup)
         tflops = r["flops_per_layer"] / (r["prefill_avg_us"] * 1e-6) / 1e12
         ms = r["wall_s"] * 1e3 / r["steps"]
-        print(json.dumps({
+        extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c4()}
+        print(json.dumps({**extra, 
             "metric": "config-4 chunked prefill attention TFLOP/s (pp512 after 0/256/1024/2048 rows, B=4)",
             "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
@@ -619,7 +674,8 @@ def main() -> int:
         r = c5_workload(dev, args.steps, args.warmup)
         gbs = r["alg_bytes_per_layer"] / (r["verify_avg_us"] * 1e-6) / 1e9
         ms = r["wall_s"] * 1e3 / r["steps"]
-        print(json.dumps({
+        extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c5()}
+        print(json.dumps({**extra, 
             "metric": "config-5 tree-verify attention GB/s (B=64, ctx U[4096,32768], 9-node tree)",
             "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
