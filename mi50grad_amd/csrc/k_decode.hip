@@ -59,12 +59,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const char *base, ui
 }
 
 // Load a half page (kb, vb: the page's first row, this head's 512 bytes;
-// koff/voff already hold this wave's first row).  Full (or disabled) pages
-// carry the row offset in soffset; a partial page puts it in voffset so the
-// range check (num_records = valid rows * row_bytes) returns zeros for the
-// rows past the sequence's end without touching memory, and a disabled page
-// (num_records = 0) fetches nothing.  Both forms issue the same loads, so the
-// compiler's load counters stay exact across the branch.
+// koff/voff already hold this wave's first row).  One branch-free form for
+// every page: each row offset travels in voffset, and the resource's range
+// (num_records = valid rows * row_bytes) makes the rows past the sequence's
+// end read as zeros without touching memory; a disabled page (num_records =
+// 0) fetches nothing.  Every step issues the same loads, so the compiler's
+// load counters stay exact (a branch between two load forms made it drain
+// the loads in flight).
 __device__ __forceinline__ void load_half(HalfPage &p, const char *kb, const char *vb, int lim, bool on,
                                           uint32_t koff, uint32_t voff, int row_bytes) {
     const uint32_t n = on ? static_cast<uint32_t>(lim * row_bytes) : 0u;
