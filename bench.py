@@ -149,12 +149,14 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
 
 
 def proj_workload(dev, steps, warmup, hidden=5120):
-    """The config-3 step with its producer: per layer, kva_project_append
-    (the Q+Q_gate and K+V projections of the 32 new tokens from hidden
-    5120, norm + RoPE, K/V into the pages) then kva_decode_gated.  Each
-    layer has its own weights (16 x 147 MB, so no layer's weights are still
-    cached when it comes round again); their values are a 32 MiB random
-    tile repeated on the device."""
+    """The config-3 step with its producer and consumer: per layer,
+    kva_project_append (the Q+Q_gate and K+V projections of the 32 new
+    tokens from hidden 5120, norm + RoPE, K/V into the pages), then
+    kva_decode_gated, then kva_out_project (the O-projection from 6144 back
+    to 5120, added into the layer's hidden rows in place).  Each layer has
+    its own weights (16 x 147 MB + 16 x 63 MB, so no layer's weights are
+    still cached when it comes round again); their values are a 32 MiB
+    random tile repeated on the device."""
     spec = wl.c3_spec(0)
     lengths, block_ids, n_blocks = spec.lengths, spec.block_ids, spec.n_blocks
     B = len(lengths)
@@ -172,10 +174,12 @@ def proj_workload(dev, steps, warmup, hidden=5120):
     tile = (rng.standard_normal(16 * 1024 * 1024, dtype=np.float32) / np.sqrt(hidden)).astype(np.float16)
     d_tile = dev.array(tile)
     nq, nkv = 2 * H * D * hidden * 2, 2 * HKV * D * hidden * 2  # bytes
+    q_dim = H * D
+    no = hidden * q_dim * 2  # O-projection weight bytes
     layers = []
     for layer in range(LAYERS):
         w = []
-        for nbytes in (nq, nkv):
+        for nbytes in (nq, nkv, no):
             d = dev.empty((nbytes // 2,), np.float16)
             off = 0
             while off < nbytes:
@@ -186,7 +190,7 @@ def proj_workload(dev, steps, warmup, hidden=5120):
         x = dev.array(wl.normal_f16(rng, (B, hidden)))
         qw, kw = dev.array(wl.norm_weight(rng)), dev.array(wl.norm_weight(rng))
         q, g, out = (dev.empty((B, H, D), np.float16) for _ in range(3))
-        layers.append((x, w[0], w[1], qw, kw, q, g, out))
+        layers.append((x, w[0], w[1], w[2], qw, kw, q, g, out))
     d_tile.free()
     seqs, ones = list(range(B)), [1] * B
 
@@ -194,7 +198,7 @@ def proj_workload(dev, steps, warmup, hidden=5120):
         for b in seqs:
             cache.set_len(b, int(lengths[b]))
         cache.begin_step(seqs, ones)
-        for layer, (x, wq, wkv, qw, kw, q, g, out) in enumerate(layers):
+        for layer, (x, wq, wkv, wo, qw, kw, q, g, out) in enumerate(layers):
             if evs is not None:
                 evs[layer][0].record()
             cache.project_append(layer, x, hidden, wq, wkv, qw, kw, d_cos, d_sin, rows, q, g)
@@ -203,11 +207,14 @@ def proj_workload(dev, steps, warmup, hidden=5120):
             cache.decode(layer, q, out, gate=g)
             if evs is not None:
                 evs[layer][2].record()
+            cache.out_project(out, B, q_dim, wo, hidden, x, residual=x)  # hidden += o_proj(attn)
+            if evs is not None:
+                evs[layer][3].record()
 
     for _ in range(warmup):
         step()
     dev.synchronize()
-    evs = [[[Event(), Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
+    evs = [[[Event(), Event(), Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
         step(evs[i])
@@ -215,11 +222,14 @@ def proj_workload(dev, steps, warmup, hidden=5120):
     wall = time.perf_counter() - t0
     proj_ms = [e[0].elapsed_ms(e[1]) for s_ in evs for e in s_]
     dec_ms = [e[1].elapsed_ms(e[2]) for s_ in evs for e in s_]
+    out_ms = [e[2].elapsed_ms(e[3]) for s_ in evs for e in s_]
     cache.destroy()
     alg = (nq + nkv) + B * hidden * 2 + 2 * B * H * D * 2 + B * 2 * HKV * D * 2
+    alg_out = no + B * q_dim * 2 + 2 * B * hidden * 2  # W_o, attention rows, hidden read + written
     return {"wall_s": wall, "steps": steps, "B": B, "hidden": hidden, "alg_bytes_proj": alg,
             "weight_bytes": nq + nkv, "proj_avg_us": float(np.mean(proj_ms) * 1e3),
-            "decode_avg_us": float(np.mean(dec_ms) * 1e3)}
+            "decode_avg_us": float(np.mean(dec_ms) * 1e3), "out_avg_us": float(np.mean(out_ms) * 1e3),
+            "alg_bytes_out": alg_out}
 
 
 def _cpu_model() -> str:
@@ -647,6 +657,10 @@ def main() -> int:
             "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
             "config": {"workload": "C3 + producer", "layers": LAYERS, "batch": r["B"], "hidden": r["hidden"]},
             "tok_per_s": r["B"] * r["steps"] / r["wall_s"], "decode_gated_avg_us": r["decode_avg_us"],
+            "out_project": {"avg_us": r["out_avg_us"], "alg_bytes_per_launch": r["alg_bytes_out"],
+                            "gbs": r["alg_bytes_out"] / (r["out_avg_us"] * 1e-6) / 1e9,
+                            "kernel": "kva_out_project = proj_lds_kernel<2 token tiles, 8 waves, 5 row tiles, "
+                                      "6 k-steps, 6 stages> + oproj_finish_kernel"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("project_c3_traffic.json"),
                          "kernel": "kva_project_append = proj_lds_kernel<2 token tiles, 8 waves, 7 row tiles, "

@@ -177,6 +177,20 @@ int kva_project_append(kva_cache *cache, int32_t layer, const void *x, int32_t h
                        const void *q_norm_w, const void *k_norm_w,
                        const void *cos_tab, const void *sin_tab, int32_t table_rows,
                        void *q_out, void *q_gate_out, void *kv_out, kva_stream_t stream);
+/* Output projection of the (gated) attention rows, the consumer of
+ * kva_decode_gated: out[t] = fp16(attn[t] . W_o^T + residual[t]) for
+ * t < n_tok, accumulated in fp32 and rounded once after the residual add.
+ * Replaces the single-GPU O-projection _launch_gemv_fp16(d_hidden,
+ * d_attn_out, o_weight, q_dim, hidden, residual=d_hidden) (engine.py:2083-
+ * 2085, launcher engine.py:2434-2455, kernel gemv_fp16_v2.hip:22-87) for
+ * all n_tok rows at once.  attn [n_tok, q_dim], w_o [n_out, q_dim] (row
+ * major), residual and out [n_tok, n_out], fp16, 16-byte aligned; residual
+ * may be NULL (no add) or equal to out (in place).  q_dim a multiple of 512,
+ * n_out a multiple of 16 and at most (2*num_heads + 2*num_kv_heads)*256
+ * (the projection workspace).  Uses no step state.                        */
+int kva_out_project(kva_cache *cache, const void *attn, int32_t n_tok, int32_t q_dim,
+                    const void *w_o, int32_t n_out, const void *residual, void *out,
+                    kva_stream_t stream);
 /* GQA decode attention, one query token per sequence (every n_new == 1):
  * out[b] = softmax(q[b] K^T / 16) V over the sequence's rows [0, len).
  * Replaces flash_attn_256_decode (flash_attn_256_tuned.hip:198-350) as

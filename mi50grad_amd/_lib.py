@@ -68,6 +68,7 @@ SIGNATURES = {
     "kva_step_begin": [_P, _I, _PI, _PI, _PI, POINTER(c_uint64), _P],
     "kva_append_qknorm_rope": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P],
     "kva_project_append": [_P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P],
+    "kva_out_project": [_P, _P, _I, _I, _P, _I, _P, _P, _P],
     "kva_decode": [_P, _I, _P, _P, _P],
     "kva_decode_gated": [_P, _I, _P, _P, c_int64, _P, _P],
     "kva_prefill": [_P, _I, _P, _P, _P],

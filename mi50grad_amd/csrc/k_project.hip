@@ -356,19 +356,63 @@ __global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
     }
 }
 
-}  // namespace
+// Grid: 8 consecutive output rows of one token per thread.  y = fp16(the
+// split partials summed in split order + residual): one rounding after the
+// residual add, the epilogue of the reference GEMV (gemv_fp16_v2.hip:81-86).
+// A thread reads its residual before writing the same 16 bytes, so the
+// residual may be the output (in place, d_hidden += o_proj(attn)).
+__global__ __launch_bounds__(256) void oproj_finish_kernel(ProjectArgs a) {
+    const int per_tok = a.n_a / 8;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.n_tok * per_tok) return;
+    const int tc = i / per_tok;
+    const size_t N = static_cast<size_t>(a.n_a);
+    const size_t row = static_cast<size_t>(i - tc * per_tok) * 8;
+    const size_t at = static_cast<size_t>(a.tok0 + tc) * N + row;
+    const uint4 r = a.residual ? ld16(a.residual + at) : make_uint4(0, 0, 0, 0);
+    const size_t split_stride = static_cast<size_t>(a.n_tok) * N;
+    const float *p = a.part + static_cast<size_t>(tc) * N + row;
+    float4_t plo[kProjMaxSplits], phi[kProjMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kProjMaxSplits; ++s) {
+        const float *ps = p + (s < a.splits ? s : 0) * split_stride;
+        plo[s] = *reinterpret_cast<const float4_t *>(ps);
+        phi[s] = *reinterpret_cast<const float4_t *>(ps + 4);
+    }
+    float4_t lo = plo[0], hi = phi[0];
+#pragma unroll
+    for (int s = 1; s < kProjMaxSplits; ++s) {
+        lo = s < a.splits ? lo + plo[s] : lo;
+        hi = s < a.splits ? hi + phi[s] : hi;
+    }
+    if (a.residual) {
+        lo += float4_t{lo_f(r.x), hi_f(r.x), lo_f(r.y), hi_f(r.y)};
+        hi += float4_t{lo_f(r.z), hi_f(r.z), lo_f(r.w), hi_f(r.w)};
+    }
+    uint4 y;
+    y.x = pack_h2(lo[0], lo[1]);
+    y.y = pack_h2(lo[2], lo[3]);
+    y.z = pack_h2(hi[0], hi[1]);
+    y.w = pack_h2(hi[2], hi[3]);
+    st16(a.y_out + at, y);
+}
 
-hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
-    if (a.n_tok <= 0) return hipSuccess;
-    constexpr int W = kProjWaves, P = kProjDepth, RT = kProjRowTiles;
-    const int n_grp = ((a.n_a + a.n_b) / 16 + RT - 1) / RT;
-    const dim3 grid(static_cast<unsigned>(n_grp * a.splits));
+// Split-K partials of x [n_tok][hidden] against the stacked weight rows.
+hipError_t launch_proj_gemm(const ProjectArgs &a, hipStream_t s) {
+    constexpr int W = kProjWaves, P = kProjDepth, RT = kProjRowTiles, LD = kProjLdsDepth;
+    const int n_t16 = (a.n_a + a.n_b) / 16;
+    const dim3 grid(static_cast<unsigned>((n_t16 + RT - 1) / RT * a.splits));
     const dim3 block(64 * W);
     const int ntb = (a.n_tok + 15) / 16;
     if (ntb <= 2 && a.hidden == kProjStreamSteps * 32 * W * a.splits) {
-        constexpr int ST = kProjStreamSteps, LD = kProjLdsDepth;
+        constexpr int ST = kProjStreamSteps;
         if (ntb == 1) hipLaunchKernelGGL((proj_lds_kernel<1, W, RT, ST, LD>), grid, block, 0, s, a);
         else hipLaunchKernelGGL((proj_lds_kernel<2, W, RT, ST, LD>), grid, block, 0, s, a);
+    } else if (ntb <= 2 && a.hidden == kProjStreamStepsB * 32 * W * a.splits) {
+        constexpr int ST = kProjStreamStepsB, RB = kProjRowTilesB;
+        const dim3 grid_b(static_cast<unsigned>((n_t16 + RB - 1) / RB * a.splits));
+        if (ntb == 1) hipLaunchKernelGGL((proj_lds_kernel<1, W, RB, ST, LD>), grid_b, block, 0, s, a);
+        else hipLaunchKernelGGL((proj_lds_kernel<2, W, RB, ST, LD>), grid_b, block, 0, s, a);
     } else switch (ntb) {
         case 1: hipLaunchKernelGGL((proj_gemm_kernel<1, W, P, RT>), grid, block, 0, s, a); break;
         case 2: hipLaunchKernelGGL((proj_gemm_kernel<2, W, P, RT>), grid, block, 0, s, a); break;
@@ -376,8 +420,27 @@ hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
         case 4: hipLaunchKernelGGL((proj_gemm_kernel<4, W, P, RT>), grid, block, 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
+    if (a.n_tok <= 0) return hipSuccess;
+    const hipError_t e = launch_proj_gemm(a, s);
+    if (e != hipSuccess) return e;
     const int blocks_per_tok = (2 * a.num_heads + 2 * a.num_kv_heads + 7) / 8;
     hipLaunchKernelGGL(proj_finish_kernel, dim3(a.n_tok * blocks_per_tok), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_out_project(const ProjectArgs &a, hipStream_t s) {
+    if (a.n_tok <= 0) return hipSuccess;
+    if (a.n_b != 0 || a.n_a % 16 != 0) return hipErrorInvalidValue;
+    const hipError_t e = launch_proj_gemm(a, s);
+    if (e != hipSuccess) return e;
+    const int threads = a.n_tok * (a.n_a / 8);
+    hipLaunchKernelGGL(oproj_finish_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

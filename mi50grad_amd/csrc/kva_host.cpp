@@ -968,6 +968,54 @@ int kva_project_append(kva_cache *c, int32_t layer, const void *x, int32_t hidde
     return capture_note(c, rc);
 }
 
+static int out_project_impl(kva_cache *c, const void *attn, int32_t n_tok, int32_t q_dim, const void *w_o,
+                            int32_t n_out, const void *residual, void *out, kva_stream_t stream) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if (n_tok < 0) return fail(KVA_ERR_INVALID_ARG, "n_tok %d is negative", n_tok);
+    if (n_tok == 0) return KVA_OK;
+    if (!attn || !w_o || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
+    if (!aligned16(attn) || !aligned16(w_o) || !aligned16(residual) || !aligned16(out))
+        return fail(KVA_ERR_MISALIGNED, "attn, w_o, residual and out must be 16-byte aligned");
+    if (q_dim <= 0 || q_dim % kva::kProjHiddenQuantum != 0)
+        return fail(KVA_ERR_INVALID_ARG, "q_dim %d must be a positive multiple of %d", q_dim,
+                    kva::kProjHiddenQuantum);
+    if (static_cast<int64_t>(kva::kProjTokens) * q_dim * 2 > INT32_MAX)
+        return fail(KVA_ERR_INVALID_ARG, "q_dim %d too large", q_dim);
+    if (n_out <= 0 || n_out % 16 != 0)
+        return fail(KVA_ERR_INVALID_ARG, "n_out %d must be a positive multiple of 16", n_out);
+    if (static_cast<int64_t>(n_tok) * n_out > INT32_MAX)
+        return fail(KVA_ERR_INVALID_ARG, "n_tok x n_out too large");
+    kva::ProjectArgs a{};
+    a.w_a = static_cast<const uint16_t *>(w_o);
+    a.w_b = a.w_a;
+    a.n_a = n_out;
+    a.n_b = 0;
+    a.hidden = q_dim;
+    a.splits = project_splits(c, q_dim, n_out);
+    if (static_cast<size_t>(a.splits) * kva::kProjTokens * n_out > c->proj_floats)
+        return fail(KVA_ERR_INVALID_ARG, "n_out %d exceeds the projection workspace (%zu floats)", n_out,
+                    c->proj_floats);
+    a.part = c->d_proj;
+    a.y_out = static_cast<uint16_t *>(out);
+    a.residual = static_cast<const uint16_t *>(residual);
+    const auto *xs = static_cast<const uint16_t *>(attn);
+    for (int32_t t0 = 0; t0 < n_tok; t0 += kva::kProjTokens) {
+        a.tok0 = t0;
+        a.n_tok = std::min(kva::kProjTokens, n_tok - t0);
+        a.x = xs + static_cast<size_t>(t0) * q_dim;
+        KVA_HIP(kva::launch_out_project(a, static_cast<hipStream_t>(stream)));
+    }
+    return KVA_OK;
+}
+
+int kva_out_project(kva_cache *c, const void *attn, int32_t n_tok, int32_t q_dim, const void *w_o, int32_t n_out,
+                    const void *residual, void *out, kva_stream_t stream) {
+    int rc = capture_check(c, stream);
+    if (rc) return capture_note(c, rc);
+    return capture_note(c, out_project_impl(c, attn, n_tok, q_dim, w_o, n_out, residual, out, stream));
+}
+
 int kva_decode(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
     int rc = capture_check(c, stream);
     if (rc) return capture_note(c, rc);

@@ -54,6 +54,11 @@ constexpr int kProjHiddenQuantum = 512;  // hidden must be a multiple of this
 constexpr int kProjWgPerCu = 1;     // GEMM workgroups per CU the split aims for, at most
 constexpr int kProjStreamSteps = 10;  // k-steps per wave of the x-resident form (up to 32 tokens)
 constexpr int kProjLdsDepth = 6;      // two-step LDS stages in flight per wave there
+// The same form over 6 k-steps per wave (hidden 6144 at four splits: the
+// O-projection from 24 heads), with 5 row tiles per workgroup so that 5120
+// output rows still make 256 workgroups.
+constexpr int kProjStreamStepsB = 6;
+constexpr int kProjRowTilesB = 5;
 struct ProjectArgs {
     const uint16_t *x;        // [n_tok][hidden], this chunk's first token
     const uint16_t *w_a;
@@ -82,8 +87,13 @@ struct ProjectArgs {
     int32_t num_kv_heads;
     int32_t half_rot;
     float eps;
+    // Output projection (launch_out_project; w_a = W_o, n_b = 0): y_out =
+    // fp16(x W_o^T + residual), both [T][n_a]; residual nullable, may be y_out.
+    uint16_t *y_out;
+    const uint16_t *residual;
 };
 hipError_t launch_project(const ProjectArgs &a, hipStream_t s);
+hipError_t launch_out_project(const ProjectArgs &a, hipStream_t s);
 
 // Reference-compatible norm+RoPE on a contiguous [n_heads][head_dim] buffer.
 struct LegacyNormArgs {

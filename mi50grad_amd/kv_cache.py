@@ -159,6 +159,15 @@ class PagedKVCache:
                   _ptr(w_kv_fused), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab),
                   table_rows, _ptr(q_out), _ptr(q_gate_out), _ptr(kv_out), stream)
 
+    def out_project(self, attn, n_tok: int, q_dim: int, w_o, n_out: int, out, residual=None,
+                    stream=None) -> None:
+        """O-projection of n_tok attention rows: out = fp16(attn . w_o^T +
+        residual), the reference's _launch_gemv_fp16(d_hidden, d_attn_out,
+        o_weight, q_dim, hidden, residual=d_hidden) (engine.py:2083-2085)
+        for every row at once.  residual may be None or `out` itself."""
+        _lib.call("kva_out_project", self.handle, _ptr(attn), n_tok, q_dim, _ptr(w_o), n_out,
+                  _ptr(residual), _ptr(out), stream)
+
     def decode(self, layer: int, q, out, stream=None, gate=None, gate_stride: int = 0) -> None:
         """Decode attention; with `gate`, the output gate (out *= sigmoid(gate),
         sigmoid_mul.hip) is applied in the same launch."""

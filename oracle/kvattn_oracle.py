@@ -71,6 +71,18 @@ def project_fp16(x: np.ndarray, w: np.ndarray) -> np.ndarray:
     return acc.astype(np.float16)
 
 
+def out_project(attn: np.ndarray, w_o: np.ndarray, residual: np.ndarray | None = None) -> np.ndarray:
+    """out[t, n] = fp16(sum_k w_o[n, k] attn[t, k] + residual[t, n]): the
+    O-projection GEMV with its residual epilogue (gemv_fp16_v2.hip:81-84,
+    called at engine.py:2083-2085 with residual = d_hidden), one fp16
+    rounding after the add.  Summed in float64 as in project_fp16; without
+    a residual it is project_fp16."""
+    acc = np.asarray(attn, np.float64) @ np.asarray(w_o, np.float64).T
+    if residual is not None:
+        acc = acc + np.asarray(residual, np.float64)
+    return acc.astype(np.float16)
+
+
 def project_append(x, w_q_fused, w_kv_fused, q_w, k_w, cos_rows, sin_rows,
                    num_heads: int = NUM_HEADS, num_kv_heads: int = NUM_KV_HEADS):
     """The reference's producer for one step, token by token: the Q+Q_gate

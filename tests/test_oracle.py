@@ -387,6 +387,40 @@ def test_project_fp16_pins():
     assert np.array_equal(orc.project_fp16(xi, wi).view(np.uint16), f32.astype(np.float16).view(np.uint16))
 
 
+def test_out_project_pins():
+    """The O-projection's residual epilogue (gemv_fp16_v2.hip:81-84): exact
+    rational brute force with the residual inside the one rounding (adding
+    it after a first rounding fails), no residual is project_fp16, a zero
+    weight returns the residual bit for bit, and unit rows add one element."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(15)
+    T, K, N = 3, 64, 9
+    x = rng.standard_normal((T, K)).astype(np.float16)
+    w = (rng.standard_normal((N, K)) * 0.2).astype(np.float16)
+    r = rng.standard_normal((T, N)).astype(np.float16)
+    want = np.empty((T, N), np.float16)
+    for t in range(T):
+        for n in range(N):
+            acc = sum((Fraction(float(w[n, k])) * Fraction(float(x[t, k])) for k in range(K)),
+                      Fraction(float(r[t, n])))
+            want[t, n] = np.float16(float(acc))
+    got = orc.out_project(x, w, r)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    big = rng.standard_normal((64, 512)).astype(np.float16)
+    wb = (rng.standard_normal((48, 512)) * 0.05).astype(np.float16)
+    rb = (rng.standard_normal((64, 48)) * 30).astype(np.float16)
+    twice_b = (orc.project_fp16(big, wb).astype(np.float32) + rb.astype(np.float32)).astype(np.float16)
+    assert not np.array_equal(orc.out_project(big, wb, rb), twice_b)
+    assert np.array_equal(orc.out_project(x, w).view(np.uint16), orc.project_fp16(x, w).view(np.uint16))
+    assert np.array_equal(orc.out_project(x, np.zeros_like(w), r).view(np.uint16), r.view(np.uint16))
+    pick = rng.integers(0, K, N)
+    wu = np.zeros((N, K), np.float16)
+    wu[np.arange(N), pick] = 1
+    sums = (x[:, pick].astype(np.float64) + r.astype(np.float64)).astype(np.float16)
+    assert np.array_equal(orc.out_project(x, wu, r).view(np.uint16), sums.view(np.uint16))
+
+
 def test_project_append_layout():
     """The producer composite reads the stacked weights the reference's way
     (engine.py:1366-1378: Q rows then Q_gate rows, K rows then V rows) and
