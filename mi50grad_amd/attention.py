@@ -70,6 +70,15 @@ class FullAttentionLaunchers:
     def _workspace(self):
         return self.kv_cache.paged.handle if self.kv_cache is not None else None
 
+    def _launch_gemv_fp16(self, dst, src, weight, K, N, residual=0, stream=0):
+        """FP16 GEMV dst[N] = weight[N, K] . src[K] (+ residual[N] when
+        non-zero, one rounding after the add): the reference launcher
+        (engine.py:2434-2455) as the O-projection uses it (engine.py:2083-
+        2085, residual = d_hidden), through kva_out_project for one row.
+        Needs the KV cache (its workspace); K a multiple of 512, N of 16."""
+        _lib.call("kva_out_project", self._workspace(), src, 1, K, weight, N, residual or None, dst,
+                  stream or self.stream)
+
     def _launch_decode_attn_256(self, out, q, k_cache, v_cache, seq_len):
         _lib.call("kva_legacy_decode", self._workspace(), q, k_cache, v_cache, out, seq_len,
                   self.local_num_attention_heads, self.local_num_kv_heads, self.stream)

@@ -115,9 +115,10 @@ def test_graph_replay_matches_eager(device, lengths, split):
 
 def test_graph_replay_project_append(device):
     """The producer path recorded too: per layer kva_project_append (fused
-    projection + norm + RoPE + append) then the gated decode, one step
-    recorded and replayed with fresh hidden states; every replay equals the
-    eager twin bit for bit, and so do the pools at the end."""
+    projection + norm + RoPE + append), the gated decode, then the
+    O-projection added into the hidden rows in place; one step recorded and
+    replayed with fresh hidden states; every replay equals the eager twin
+    bit for bit, and so do the pools at the end."""
     say("graph replay of project_append + gated decode")
     rng = np.random.default_rng(8)
     lengths, hidden = [30, 47, 3], 512
@@ -132,7 +133,8 @@ def test_graph_replay_project_append(device):
     w = [dict(wq=device.array(f16((2 * H * D, hidden), hidden ** -0.5)),
               wkv=device.array(f16((2 * HKV * D, hidden), hidden ** -0.5)),
               qw=device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)),
-              kw=device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16))) for _ in range(LAYERS)]
+              kw=device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)),
+              wo=device.array(f16((hidden, H * D), (H * D) ** -0.5))) for _ in range(LAYERS)]
     bufs = [[dict(x=device.empty((B, hidden), np.float16), q=device.empty((B, H, D), np.float16),
                   g=device.empty((B, H, D), np.float16), out=device.empty((B, H, D), np.float16))
              for _ in range(LAYERS)] for _ in range(2)]
@@ -143,6 +145,7 @@ def test_graph_replay_project_append(device):
             cache.project_append(layer, b["x"], hidden, p["wq"], p["wkv"], p["qw"], p["kw"], tables.d_cos,
                                  tables.d_sin, tables.rows, b["q"], b["g"], stream=stream_h)
             cache.decode(layer, b["q"], b["out"], stream=stream_h, gate=b["g"])
+            cache.out_project(b["out"], B, H * D, p["wo"], hidden, b["x"], residual=b["x"], stream=stream_h)
 
     graph = None
     for step in range(12):
@@ -162,7 +165,7 @@ def test_graph_replay_project_append(device):
         stream.synchronize()
         device.synchronize()
         for layer in range(LAYERS):
-            for name in ("q", "g", "out"):
+            for name in ("q", "g", "out", "x"):
                 got = bufs[1][layer][name].numpy().view(np.uint16)
                 exp = bufs[0][layer][name].numpy().view(np.uint16)
                 assert np.array_equal(got, exp), (step, layer, name)

@@ -96,3 +96,26 @@ def test_engine_style_decode_steps(device):
     exp = np.stack([orc.attention_fp32(q[b:b + 1], hist_k[b], hist_v[b])[0] for b in range(batch)])
     assert max_err(out.numpy(), exp) <= 2e-3
     kv.cleanup()
+
+
+def test_gemv_fp16_o_projection(device):
+    """engine.py:2083-2085: d_hidden = fp16(o_proj(attn) + d_hidden) in place
+    through the reference-named launcher, then without the residual."""
+    say("engine-style O-projection GEMV")
+    rng = np.random.default_rng(78)
+    cfg = AttnConfig(num_hidden_layers=4)
+    kv = KVCache(cfg, 64, device, batch_size=1)
+    eng = FullAttentionLaunchers(cfg, device, max_seq_len=64, kv_cache=kv)
+    q_dim, hidden = H * D, 512
+    attn = rng.integers(-3, 4, q_dim).astype(np.float16)
+    w = (rng.integers(-2, 3, (hidden, q_dim)) * 2.0 ** -7).astype(np.float16)
+    h0 = (rng.integers(-64, 65, hidden) * 2.0 ** -3).astype(np.float16)
+    d_attn, d_w, d_hid = device.array(attn), device.array(w), device.array(h0)
+    eng._launch_gemv_fp16(d_hid.ptr, d_attn.ptr, d_w.ptr, q_dim, hidden, residual=d_hid.ptr)
+    d_out = device.empty((hidden,), np.float16)
+    eng._launch_gemv_fp16(d_out.ptr, d_attn.ptr, d_w.ptr, q_dim, hidden)
+    device.synchronize()
+    exp = orc.out_project(attn[None], w, h0[None])[0]
+    assert np.array_equal(d_hid.numpy().view(np.uint16), exp.view(np.uint16))
+    assert np.array_equal(d_out.numpy().view(np.uint16), orc.out_project(attn[None], w)[0].view(np.uint16))
+    kv.cleanup()
