@@ -659,6 +659,7 @@ def main() -> int:
             "tok_per_s": r["B"] * r["steps"] / r["wall_s"], "decode_gated_avg_us": r["decode_avg_us"],
             "out_project": {"avg_us": r["out_avg_us"], "alg_bytes_per_launch": r["alg_bytes_out"],
                             "gbs": r["alg_bytes_out"] / (r["out_avg_us"] * 1e-6) / 1e9,
+                            "traffic": load_traffic("out_project_c3_traffic.json"),
                             "kernel": "kva_out_project = proj_lds_kernel<2 token tiles, 8 waves, 5 row tiles, "
                                       "6 k-steps, 6 stages> + oproj_finish_kernel"},
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
