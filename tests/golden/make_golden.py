@@ -59,6 +59,24 @@ def main() -> None:
         "tree7_row3": [1, 1, 0, 1, 0, 0, 0, 1, 1],
         # tests/test_tree_vs_causal_attention.py:289-322.
         "tree7_ancestor_counts": [1, 2, 2, 3, 3, 3, 3],
+        # Node depths the reference's tests assert (TreeNode.depth =
+        # parent.depth + 1, tree_attention.py:35; get_max_depth,
+        # get_nodes_at_depth): tests/test_tree_attention_mask.py:44-54 (root
+        # 0, children 1), :84-125 (root, two children, a grandchild under the
+        # first: max depth 2, one/two/one nodes at depths 0/1/2), :145-170
+        # (complete binary trees of depth 0..3), :185-212 (chains of 4 and of
+        # 1) and :225-231 (a star of 3 children).  Parent arrays in the
+        # reference's BFS numbering.
+        "tree_depth_cases": [
+            {"parents": [-1, 0, 0], "depths": [0, 1, 1]},
+            {"parents": [-1, 0, 0, 1], "max_depth": 2, "nodes_per_depth": [1, 2, 1]},
+            {"parents": [-1], "max_depth": 0},
+            {"parents": [-1, 0, 0], "max_depth": 1},
+            {"parents": [-1, 0, 0, 1, 1, 2, 2], "max_depth": 2},
+            {"parents": [-1] + [(i - 1) // 2 for i in range(1, 15)], "max_depth": 3},
+            {"parents": [-1, 0, 1, 2], "max_depth": 3},
+            {"parents": [-1, 0, 0, 0], "max_depth": 1},
+        ],
     }
     (HERE / "golden.json").write_text(json.dumps(golden, indent=1) + "\n")
 

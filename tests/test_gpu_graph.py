@@ -4,18 +4,22 @@ Two caches built from the same seed: one runs every step's per-layer
 append + decode eagerly, the other records one step into a graph and replays
 it for 20 more steps, with fresh inputs uploaded between replays (the eager
 work and synchronizations between them), lengths crossing page boundaries
-(so the decode's stream-K shape changes under the recording) and a decode
-split set.  Every replayed step's outputs and, at the end, every pool byte
-must equal the eager twin's.  Also: what recording refuses, and a replay
-whose step has another shape.
+(so the decode's stream-K shape, derived on the device from the step plan,
+changes under the recording) and a decode split set.  Every replayed step's
+outputs and, at the end, every pool byte must equal the eager twin's, and
+every replayed output is also compared with the oracle (attention over the
+oracle's own copy of the rows within 2e-3; O-projection within one fp16 ulp
+of ``orc.out_project`` on the replay's own gated rows).  Also: what
+recording refuses, and a replay whose step has another shape.
 """
 import numpy as np
 import pytest
 
 from mi50grad_amd._lib import KvaError
 from mi50grad_amd.device import Stream
+from oracle import kvattn_oracle as orc
 
-from gpu_helpers import HKV, H, D, Tables, build_cache, say
+from gpu_helpers import HKV, H, D, Tables, build_cache, expected_norm, max_err, say
 
 pytestmark = pytest.mark.gpu
 LAYERS = 3
@@ -29,22 +33,27 @@ def _twin(lengths, split, seed):
         o += n
     caches = []
     for _ in range(2):
-        c, _, _ = build_cache(lengths, ids, extra_rows=40, n_layers=LAYERS, rng=np.random.default_rng(seed))
+        c, kr, vr = build_cache(lengths, ids, extra_rows=40, n_layers=LAYERS, rng=np.random.default_rng(seed))
         c.set_decode_split(split)
         caches.append(c)
-    return caches
+    # The oracle's copy of every layer's rows, per sequence (appended to as
+    # the steps run).
+    hist = [[(list(kr[layer][b]), list(vr[layer][b])) for b in range(len(lengths))] for layer in range(LAYERS)]
+    return caches, hist
 
 
 @pytest.mark.parametrize("lengths,split", [([14, 30], 0), ([200, 5, 77], 32)])
 def test_graph_replay_matches_eager(device, lengths, split):
     say(f"graph replay lengths={lengths} split={split}")
     rng = np.random.default_rng(5)
-    eager, graphed = _twin(lengths, split, seed=11)
+    (eager, graphed), hist = _twin(lengths, split, seed=11)
     B = len(lengths)
     tables = Tables(device, 512)
     stream = Stream()
-    qw = [device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)) for _ in range(LAYERS)]
-    kw = [device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)) for _ in range(LAYERS)]
+    h_qw = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float16) for _ in range(LAYERS)]
+    h_kw = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float16) for _ in range(LAYERS)]
+    qw = [device.array(w) for w in h_qw]
+    kw = [device.array(w) for w in h_kw]
 
     def fresh(shape):
         return rng.standard_normal(shape, dtype=np.float32).astype(np.float16)
@@ -90,12 +99,21 @@ def test_graph_replay_matches_eager(device, lengths, split):
         graph.launch()
         stream.synchronize()
         device.synchronize()
+        pos = [L + step for L in lengths]
         for layer in range(LAYERS):
-            got = bufs[1][layer]["out"].numpy().view(np.uint16)
-            exp = bufs[0][layer]["out"].numpy().view(np.uint16)
-            assert np.array_equal(got, exp), (step, layer)
+            got = bufs[1][layer]["out"].numpy()
+            exp = bufs[0][layer]["out"].numpy()
+            assert np.array_equal(got.view(np.uint16), exp.view(np.uint16)), (step, layer)
             assert np.array_equal(bufs[1][layer]["q"].numpy().view(np.uint16),
                                   bufs[0][layer]["q"].numpy().view(np.uint16)), (step, layer)
+            qn = expected_norm(inputs[layer]["q"], h_qw[layer], tables, pos)
+            kn = expected_norm(inputs[layer]["k"], h_kw[layer], tables, pos)
+            for b in range(B):
+                hist[layer][b][0].append(kn[b])
+                hist[layer][b][1].append(inputs[layer]["v"][b])
+            ora = orc.decode_attention(qn, [np.stack(hist[layer][b][0]) for b in range(B)],
+                                       [np.stack(hist[layer][b][1]) for b in range(B)])
+            assert max_err(got, ora) <= 2e-3, (step, layer)
     for layer in range(LAYERS):
         ke, ve = eager.download_pools(layer)
         kg, vg = graphed.download_pools(layer)
@@ -122,7 +140,7 @@ def test_graph_replay_project_append(device):
     say("graph replay of project_append + gated decode")
     rng = np.random.default_rng(8)
     lengths, hidden = [30, 47, 3], 512
-    eager, graphed = _twin(lengths, 0, seed=12)
+    (eager, graphed), hist = _twin(lengths, 0, seed=12)
     B = len(lengths)
     tables = Tables(device, 512)
     stream = Stream()
@@ -130,11 +148,11 @@ def test_graph_replay_project_append(device):
     def f16(shape, s=1.0):
         return (rng.standard_normal(shape, dtype=np.float32) * s).astype(np.float16)
 
-    w = [dict(wq=device.array(f16((2 * H * D, hidden), hidden ** -0.5)),
-              wkv=device.array(f16((2 * HKV * D, hidden), hidden ** -0.5)),
-              qw=device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)),
-              kw=device.array((1 + 0.02 * rng.standard_normal(D)).astype(np.float16)),
-              wo=device.array(f16((hidden, H * D), (H * D) ** -0.5))) for _ in range(LAYERS)]
+    hw = [dict(wq=f16((2 * H * D, hidden), hidden ** -0.5), wkv=f16((2 * HKV * D, hidden), hidden ** -0.5),
+               qw=(1 + 0.02 * rng.standard_normal(D)).astype(np.float16),
+               kw=(1 + 0.02 * rng.standard_normal(D)).astype(np.float16),
+               wo=f16((hidden, H * D), (H * D) ** -0.5)) for _ in range(LAYERS)]
+    w = [{name: device.array(a) for name, a in p.items()} for p in hw]
     bufs = [[dict(x=device.empty((B, hidden), np.float16), q=device.empty((B, H, D), np.float16),
                   g=device.empty((B, H, D), np.float16), out=device.empty((B, H, D), np.float16))
              for _ in range(LAYERS)] for _ in range(2)]
@@ -169,6 +187,28 @@ def test_graph_replay_project_append(device):
                 got = bufs[1][layer][name].numpy().view(np.uint16)
                 exp = bufs[0][layer][name].numpy().view(np.uint16)
                 assert np.array_equal(got, exp), (step, layer, name)
+        # The replay against the oracle, layer 0: projection + norm + RoPE
+        # (within one fp16 ulp: random sums), gated attention over the
+        # oracle's rows (2e-3), and the O-projection of the replay's own
+        # gated rows plus the residual (one ulp).
+        pos = [L + step for L in lengths]
+        cos, sin = tables.cos[pos], tables.sin[pos]
+        p = hw[0]
+        q_o, g_o, _, k_o, v_o = orc.project_append(xs[0], p["wq"], p["wkv"], p["qw"], p["kw"], cos, sin)
+        q_g = bufs[1][0]["q"].numpy()
+        assert max_err(q_g, q_o) <= 2 * np.max(np.abs(q_o.astype(np.float32))) * 2.0 ** -10 + 2.0 ** -12, step
+        assert max_err(bufs[1][0]["g"].numpy(), g_o) <= np.max(np.abs(g_o.astype(np.float32))) * 2.0 ** -10 + 2.0 ** -12, step
+        for b in range(B):
+            hist[0][b][0].append(k_o[b])
+            hist[0][b][1].append(v_o[b])
+        att = orc.decode_attention(q_g, [np.stack(hist[0][b][0]) for b in range(B)],
+                                   [np.stack(hist[0][b][1]) for b in range(B)])
+        gated = orc.sigmoid_gate(att.astype(np.float16), bufs[1][0]["g"].numpy())
+        out_g = bufs[1][0]["out"].numpy()
+        assert max_err(out_g, gated) <= 2e-3, step
+        x_exp = orc.out_project(out_g.reshape(B, H * D), p["wo"], xs[0])
+        x_got = bufs[1][0]["x"].numpy()
+        assert max_err(x_got, x_exp) <= np.max(np.abs(x_exp.astype(np.float32))) * 2.0 ** -10 + 2.0 ** -12, step
     for layer in range(LAYERS):
         ke, ve = eager.download_pools(layer)
         kg, vg = graphed.download_pools(layer)

@@ -167,7 +167,10 @@ def test_tree_verify_append_then_rollback(device):
     say("tree verify + rollback")
     cache, kr, vr = build_cache(lengths, ids, extra_rows=9, n_layers=n_layers, rng=rng)
     tables = Tables(device, 6000)
-    depth = tr.depths(C5_PARENTS)
+    # RoPE positions len + depth, from the oracle's depths (the kernel input
+    # and the expectation alike; the product's own depths are checked in
+    # test_gpu_speculative against these).
+    depth = orc.tree_depths(C5_PARENTS).tolist()
     rope_pos = [L + d for L in lengths for d in depth]
     T = 9 * B
     outs, qns, kns, vs = [], [], [], []

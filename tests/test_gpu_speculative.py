@@ -42,6 +42,10 @@ def _run_step(device, cache, rng, tables, trees, n_layers, k_hist, v_hist):
     (each sequence's rows before the step)."""
     step = sp.TreeVerifyStep(cache, list(range(len(trees))), trees)
     T = step.n_tokens
+    # Expected RoPE positions len + depth from the oracle's depths; the
+    # product's (which the kernels were given) must agree.
+    exp_pos = [len(k_hist[0][b]) + int(d) for b, par in enumerate(trees) for d in orc.tree_depths(par)]
+    assert list(step.rope_pos) == exp_pos
     kns, vs = [], []
     for layer in range(n_layers):
         q = rng.standard_normal((T, H, D), dtype=np.float32).astype(np.float16)
@@ -54,8 +58,8 @@ def _run_step(device, cache, rng, tables, trees, n_layers, k_hist, v_hist):
                      tables.d_cos, tables.d_sin, tables.rows)
         cache.tree_verify(layer, dq, out)
         device.synchronize()
-        qn = expected_norm(q, qw, tables, step.rope_pos)
-        kn = expected_norm(k, kw, tables, step.rope_pos)
+        qn = expected_norm(q, qw, tables, exp_pos)
+        kn = expected_norm(k, kw, tables, exp_pos)
         got = out.numpy()
         for b, par in enumerate(trees):
             s = step.rows_of(b)

@@ -225,6 +225,35 @@ def test_tree_mask_known_answers():
     assert counts == g["tree7_ancestor_counts"]
 
 
+def test_tree_depths_pinned():
+    """oracle.tree_depths, the RoPE offset of tree rows (position len + depth):
+    the depths the reference's own tests assert, config 5's tree, and closed
+    forms (a chain is arange; a complete binary tree in BFS order puts node i
+    at floor(log2(i + 1))).  Depth as the number of ancestors is checked too,
+    so an off-by-one (root at 1) or a parent-index mix-up fails."""
+    for case in golden()["tree_depth_cases"]:
+        d = orc.tree_depths(case["parents"]).tolist()
+        if "depths" in case:
+            assert d == case["depths"]
+        if "max_depth" in case:
+            assert max(d) == case["max_depth"]
+        if "nodes_per_depth" in case:
+            assert [d.count(k) for k in range(max(d) + 1)] == case["nodes_per_depth"]
+    assert orc.tree_depths([-1, 0, 0, 0, 1, 1, 2, 4, 4]).tolist() == [0, 1, 1, 1, 2, 2, 2, 3, 3]
+    assert orc.tree_depths([-1] + list(range(11))).tolist() == list(range(12))
+    binary = [-1] + [(i - 1) // 2 for i in range(1, 63)]
+    assert orc.tree_depths(binary).tolist() == [int(np.floor(np.log2(i + 1))) for i in range(63)]
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        n = int(rng.integers(1, 40))
+        parents = [-1] + [int(rng.integers(0, i)) for i in range(1, n)]
+        assert orc.tree_depths(parents).tolist() == [len(orc.tree_ancestors(parents, i)) for i in range(n)]
+    with pytest.raises(AssertionError):
+        orc.tree_depths([0, 0])        # no root
+    with pytest.raises(AssertionError):
+        orc.tree_depths([-1, 2, 0])    # a parent after its child
+
+
 def test_tree_mask_invariants_and_cache_order():
     parents = [-1, 0, 0, 0, 1, 1, 2, 4, 4]
     m = orc.tree_mask_reference(parents, 5)
