@@ -280,6 +280,18 @@ int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row,
 int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base,
                       const void *v_base, void *out, int32_t kv_seq_len,
                       int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream);
+/* kva_legacy_decode without a workspace cache and without allocating: no
+ * counterpart in the reference.  It is for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results as kva_legacy_decode;
+ * the split-K partials live in a static 16 MiB device array of the library
+ * (one per GPU, held until the process ends), so num_heads is at most 128
+ * (KVA_ERR_CAPACITY beyond).  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race and must
+ * be ordered by the caller.  Nothing in the array needs to start at zero.  */
+int kva_legacy_decode_noalloc(const void *q, const void *k_base, const void *v_base,
+                              void *out, int32_t kv_seq_len, int32_t num_heads,
+                              int32_t num_kv_heads, kva_stream_t stream);
 /* kva_legacy_decode followed by the output gate (as kva_decode_gated) in
  * one call: the engine's decode + _launch_sigmoid_mul pair
  * (engine.py:2047-2056).  gate: [num_heads, 256] fp16, 8-byte aligned.     */

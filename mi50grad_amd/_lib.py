@@ -82,6 +82,7 @@ SIGNATURES = {
     "kva_graph_destroy": [_P],
     "kva_legacy_qknorm_rope": [_P, _P, _P, _P, _P, _I, _I, _I, c_float, _P],
     "kva_legacy_decode": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+    "kva_legacy_decode_noalloc": [_P, _P, _P, _P, _I, _I, _I, _P],
     "kva_legacy_decode_gated": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "kva_legacy_decode_batched": [_P, _P, _P, _P, _P, _I, _I, c_int64, _I, _I, _P],
     "kva_hbm_copy": [_P, _P, c_size_t, _P],

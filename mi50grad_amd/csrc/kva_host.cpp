@@ -1263,9 +1263,12 @@ int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row, const vo
     return KVA_OK;
 }
 
+// noalloc: take the split-K partials from the library's static device
+// scratch (kva_legacy_decode_noalloc) instead of a cache's workspace.
 static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const void *k_base, const void *v_base,
                          void *out, int32_t kv_seq_len, int32_t batch, int64_t batch_stride,
-                         int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream) {
+                         int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream,
+                         bool noalloc = false) {
     if (!q || !k_base || !v_base || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (kv_seq_len <= 0) return fail(KVA_ERR_INVALID_ARG, "kv_seq_len %d must be positive", kv_seq_len);
     if (batch <= 0 || batch > 65535) return fail(KVA_ERR_INVALID_ARG, "batch %d outside [1, 65535]", batch);
@@ -1297,7 +1300,23 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
     // Every sequence has the same length: the page prefix sums are implicit.
     const int64_t unit_pages = (kv_seq_len + kva::kBlockTokens - 1) / kva::kBlockTokens;
     const int64_t pages = unit_pages * batch;
-    if (ws) {
+    if (noalloc) {
+        if (num_heads > kva::kNoAllocMaxHeads)
+            return fail(KVA_ERR_CAPACITY, "num_heads %d: the static decode scratch (%zu bytes) serves at most %d heads",
+                        num_heads, kva::kNoAllocScratchBytes, kva::kNoAllocMaxHeads);
+        void *scratch = nullptr;
+        int n_cu = 0;
+        KVA_HIP(kva::noalloc_scratch(&scratch, &n_cu));
+        // Two partial slots of num_heads rows (256 + 2 floats) per workgroup.
+        const int64_t slot_bytes = static_cast<int64_t>(num_heads) * (kva::kHeadDim + 2) * sizeof(float);
+        const int64_t fit = static_cast<int64_t>(kva::kNoAllocScratchBytes) / (2 * slot_bytes);
+        a.total_pages = static_cast<int32_t>(pages);
+        a.n_wg = static_cast<int32_t>(std::max<int64_t>(
+            1, std::min<int64_t>({static_cast<int64_t>(n_cu) * kDecodeWgPerCu,
+                                  (pages + kMinPagesPerWg - 1) / kMinPagesPerWg, fit})));
+        a.ws_acc = static_cast<float *>(scratch);
+        a.ws_ml = a.ws_acc + static_cast<size_t>(2) * a.n_wg * num_heads * kva::kHeadDim;
+    } else if (ws) {
         set_stream_k(ws, a, pages, num_heads);
     } else {
         // No workspace: one workgroup per sequence, written whole.
@@ -1307,6 +1326,13 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;
+}
+
+int kva_legacy_decode_noalloc(const void *q, const void *k_base, const void *v_base, void *out,
+                              int32_t kv_seq_len, int32_t num_heads, int32_t num_kv_heads,
+                              kva_stream_t stream) {
+    return legacy_decode(nullptr, q, nullptr, k_base, v_base, out, kv_seq_len, 1, 0, num_heads, num_kv_heads,
+                         stream, true);
 }
 
 int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base, const void *v_base,

@@ -144,6 +144,14 @@ struct DecodeArgs {
 };
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
 
+// Static device scratch of kva_legacy_decode_noalloc (k_noalloc.hip): the
+// decode partial slots [2*n_wg][H][256] floats, then [2*n_wg][H][2].
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+constexpr int kNoAllocMaxHeads = 128;  // query heads it serves, at most
+// The current device's scratch address (fetched once per device with
+// hipGetSymbolAddress) and its CU count.
+hipError_t noalloc_scratch(void **ptr, int *n_cu);
+
 // Apply block-table patches (seq, index, block) staged by a step.
 hipError_t launch_table_patch(int32_t *table, int32_t table_stride,
                               const int32_t *patches, int32_t n_patches,
