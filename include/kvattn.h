@@ -14,7 +14,10 @@
  *   - kva_stream_t is a hipStream_t (NULL = the legacy default stream); a
  *     cache is driven from one host thread and its calls are ordered on the
  *     stream they are given: calls on different streams must be ordered by
- *     the caller;
+ *     the caller.  A cache owns one set of workspaces (decode, multi-query
+ *     and projection partials, the step plan) shared by every call on it,
+ *     so two calls on one cache that overlap on different streams race:
+ *     use one stream per cache, or one cache per stream;
  *   - the library allocates device memory only in kva_create and the
  *     kva_dev_* helpers, never inside a hot-path call.
  *
@@ -276,7 +279,9 @@ int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row,
 /* flash_attn_256_decode semantics (flash_attn_256_tuned.hip:198-350) on a
  * contiguous cache K/V [kv_seq_len, num_kv_heads, 256]: one query row
  * q [num_heads, 256] -> out [num_heads, 256].  `ws` (nullable) lends its
- * split-K workspace; with NULL the call runs one split per KV head.        */
+ * split-K workspace; with NULL the call runs one workgroup per sequence (one
+ * CU: meant for short caches; long ones take a workspace or
+ * kva_legacy_decode_noalloc).                                              */
 int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base,
                       const void *v_base, void *out, int32_t kv_seq_len,
                       int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream);

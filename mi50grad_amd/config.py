@@ -11,6 +11,7 @@ from dataclasses import dataclass, field
 
 @dataclass
 class AttnConfig:
+    hidden_size: int = 5120
     num_hidden_layers: int = 64
     num_attention_heads: int = 24
     num_key_value_heads: int = 4

@@ -158,6 +158,28 @@ __device__ __forceinline__ float group4_sum(float x) {
     return a + b;
 }
 
+// Four attention output dims o0..o3 as fp16, through the optional output
+// gate: the attention value is rounded to fp16 first and then multiplied by
+// 1/(1+exp(-g)) in float32 (sigmoid_mul.hip:10-22 applied to the attention
+// output, engine.py:2055-2056 after decode and :3120-3121 after prefill), so
+// the fused result equals the reference's two launches.  g4: the four gate
+// values (8-byte aligned) or null.
+__device__ __forceinline__ uint2 out_fp16x4(float o0, float o1, float o2, float o3, const uint16_t *g4) {
+    uint2 o;
+    o.x = pack_h2(o0, o1);
+    o.y = pack_h2(o2, o3);
+    if (!g4) return o;
+    const uint2 gw = *reinterpret_cast<const uint2 *>(g4);
+    const float g[4] = {lo_f(gw.x), hi_f(gw.x), lo_f(gw.y), hi_f(gw.y)};
+    const float a[4] = {lo_f(o.x), hi_f(o.x), lo_f(o.y), hi_f(o.y)};
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = a[i] * (1.0f / (1.0f + expf(-g[i])));
+    o.x = pack_h2(r[0], r[1]);
+    o.y = pack_h2(r[2], r[3]);
+    return o;
+}
+
 __device__ __forceinline__ uint4 ld16(const uint16_t *p) {
     return *reinterpret_cast<const uint4 *>(p);
 }

@@ -993,9 +993,11 @@ static int out_project_impl(kva_cache *c, const void *attn, int32_t n_tok, int32
     a.n_b = 0;
     a.hidden = q_dim;
     a.splits = project_splits(c, q_dim, n_out);
-    if (static_cast<size_t>(a.splits) * kva::kProjTokens * n_out > c->proj_floats)
-        return fail(KVA_ERR_INVALID_ARG, "n_out %d exceeds the projection workspace (%zu floats)", n_out,
-                    c->proj_floats);
+    // One launch pair's partials: [splits][its tokens][n_out] floats.
+    const int64_t chunk_tok = std::min(n_tok, kva::kProjTokens);
+    if (static_cast<size_t>(a.splits) * chunk_tok * n_out > c->proj_floats)
+        return fail(KVA_ERR_CAPACITY, "n_out %d x %lld tokens exceeds the projection workspace (%zu floats)", n_out,
+                    static_cast<long long>(chunk_tok), c->proj_floats);
     a.part = c->d_proj;
     a.y_out = static_cast<uint16_t *>(out);
     a.residual = static_cast<const uint16_t *>(residual);
@@ -1319,7 +1321,9 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
     } else if (ws) {
         set_stream_k(ws, a, pages, num_heads);
     } else {
-        // No workspace: one workgroup per sequence, written whole.
+        // No workspace: one workgroup per sequence, written whole (one CU
+        // per sequence: for short caches; the Python launchers always pass
+        // a workspace).
         a.total_pages = static_cast<int32_t>(pages);
         a.n_wg = batch;
     }

@@ -54,6 +54,12 @@ class GPUDevice:
     def synchronize(self) -> None:
         _lib.call("kva_dev_synchronize")
 
+    def launch_cached(self, spec, stream: int = 0) -> None:
+        """Launch a pre-built spec of the decode launch cache with its
+        current parameter values (hip_dispatch.py:681-689)."""
+        self._ensure_device()
+        spec.launch(stream or None)
+
     def cleanup(self) -> None:
         for p in list(self._allocations):
             self.free(p)

@@ -238,7 +238,8 @@ class KVCache:
         self.paged = PagedKVCache(
             n_layers=self.num_full_layers, max_seqs=batch_size,
             max_blocks=batch_size * self._pages_per_slot,
-            max_blocks_per_seq=self._pages_per_slot, max_step_tokens=max(16, batch_size * 16),
+            max_blocks_per_seq=self._pages_per_slot,
+            max_step_tokens=max(16, batch_size * 16, max_seq_len),  # a prefill of up to max_seq_len tokens
             num_heads=local_heads, num_kv_heads=self.local_num_kv_heads,
             head_dim=config.head_dim, rotary_dim=int(config.head_dim * config.partial_rotary_factor),
             eps=config.rms_norm_eps)
