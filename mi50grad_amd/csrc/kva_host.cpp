@@ -996,7 +996,7 @@ static int out_project_impl(kva_cache *c, const void *attn, int32_t n_tok, int32
     // One launch pair's partials: [splits][its tokens][n_out] floats.
     const int64_t chunk_tok = std::min(n_tok, kva::kProjTokens);
     if (static_cast<size_t>(a.splits) * chunk_tok * n_out > c->proj_floats)
-        return fail(KVA_ERR_CAPACITY, "n_out %d x %lld tokens exceeds the projection workspace (%zu floats)", n_out,
+        return fail(KVA_ERR_INVALID_ARG, "n_out %d x %lld tokens exceeds the projection workspace (%zu floats)", n_out,
                     static_cast<long long>(chunk_tok), c->proj_floats);
     a.part = c->d_proj;
     a.y_out = static_cast<uint16_t *>(out);

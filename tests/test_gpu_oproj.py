@@ -91,8 +91,12 @@ def test_out_project_errors(device):
         cache.out_project(dx, 2, 500, dw, 64, out)  # q_dim not a multiple of 512
     with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
         cache.out_project(dx, 2, 512, dw, 60, out)  # n_out not a multiple of 16
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
-        cache.out_project(dx, 2, 512, dw, 1 << 20, out)  # beyond the workspace
+    # Beyond the projection workspace for 2 tokens (2 x n_out partial floats
+    # > its 3.67 M): refused on the host.  The size must exceed the check
+    # itself, not only the buffers: a call that passed the check would run
+    # the GEMM over n_out rows of these 64-row buffers.
+    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG.*workspace"):
+        cache.out_project(dx, 2, 512, dw, 1 << 24, out)
     with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
         cache.out_project(dx, -1, 512, dw, 64, out)
     with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):

@@ -119,3 +119,231 @@ def test_gemv_fp16_o_projection(device):
     assert np.array_equal(d_hid.numpy().view(np.uint16), exp.view(np.uint16))
     assert np.array_equal(d_out.numpy().view(np.uint16), orc.out_project(attn[None], w)[0].view(np.uint16))
     kv.cleanup()
+
+
+# ---- the engine surface through install(): prefill, launch cache, rollback --
+class _Layer:
+    def __init__(self, layer_type):
+        self.layer_type = layer_type
+
+
+class StubEngine:
+    """What install() and the reference-named methods read from an
+    InferenceEngine: config, device, kv_cache, layers with the stacked
+    attention weights of engine.py:1366-1378, the decode buffers (d_q, d_k,
+    d_attn_out), the prefill buffers, and the engine's own hidden-state
+    RMSNorm and sigmoid gate (outside this path; here numpy on the host)."""
+
+    _alloc_prefill_scratch = FullAttentionLaunchers._alloc_prefill_scratch
+
+    def __init__(self, cfg, device, kv, rng, hidden):
+        self.config, self.device, self.kv_cache = cfg, device, kv
+        self.host = {}
+        self.layers = []
+        q_dim, kv_dim = H * D, HKV * D
+        for i in range(cfg.num_hidden_layers):
+            lw = _Layer("full_attention" if cfg.is_full_attention(i) else "linear_attention")
+            if lw.layer_type == "full_attention":
+                wq = (rng.standard_normal((2 * q_dim, hidden), dtype=np.float32) * hidden ** -0.5).astype(np.float16)
+                wkv = (rng.standard_normal((2 * kv_dim, hidden), dtype=np.float32) * hidden ** -0.5).astype(np.float16)
+                wo = (rng.standard_normal((hidden, q_dim), dtype=np.float32) * q_dim ** -0.5).astype(np.float16)
+                qn = (1 + 0.02 * rng.standard_normal(D)).astype(np.float16)
+                kn = (1 + 0.02 * rng.standard_normal(D)).astype(np.float16)
+                an = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float16)
+                self.host[i] = dict(wq=wq, wkv=wkv, wo=wo, qn=qn, kn=kn, an=an)
+                lw.q_fused_weight = device.array(wq).ptr
+                lw.q_weight, lw.q_gate_weight = lw.q_fused_weight, lw.q_fused_weight + q_dim * hidden * 2
+                lw.kv_fused_weight = device.array(wkv).ptr
+                lw.k_weight, lw.v_weight = lw.kv_fused_weight, lw.kv_fused_weight + kv_dim * hidden * 2
+                lw.o_weight = device.array(wo).ptr
+                lw.q_norm, lw.k_norm, lw.attn_norm = device.array(qn).ptr, device.array(kn).ptr, device.array(an).ptr
+            self.layers.append(lw)
+        self.d_q = device.malloc(q_dim * 2)
+        self.d_k = device.malloc(kv_dim * 2)
+        self.d_attn_out = device.malloc(q_dim * 2)
+
+    def _launch_sigmoid_mul(self, attn_out, gate, n):
+        a = np.frombuffer(self.device.download(attn_out, n * 2), np.float16)
+        g = np.frombuffer(self.device.download(gate, n * 2), np.float16)
+        self.device.upload(attn_out, orc.sigmoid_gate(a, g).tobytes())
+
+    def _launch_rmsnorm(self, dst, src, weight, dim):
+        x = np.frombuffer(self.device.download(src, dim * 2), np.float16).astype(np.float32)
+        w = np.frombuffer(self.device.download(weight, dim * 2), np.float16).astype(np.float32)
+        y = (x / np.sqrt(np.mean(x * x) + 1e-6) * w).astype(np.float16)
+        self.device.upload(dst, y.tobytes())
+
+    # The reference names, defined in the class body as InferenceEngine does.
+    def _prefill_full_attention(self, *a):
+        raise AssertionError("reference prefill called")
+
+    _launch_qknorm_rope = _launch_decode_attn_256 = build_decode_launch_cache = rollback_kv_cache = \
+        _prefill_full_attention
+
+
+def _ulp_close(got, exp, ulps=1):
+    """Within `ulps` fp16 ulps of each expected element, plus 2^-12 for the
+    fp32 accumulation of the projection (its error is absolute: a sum that
+    cancels to a tiny value is not known to a few of ITS ulps)."""
+    e = np.abs(np.asarray(exp, np.float32))
+    return np.all(np.abs(np.asarray(got, np.float32) - exp.astype(np.float32)) <= ulps * np.maximum(e, 2.0 ** -14) * 2.0 ** -10 + 2.0 ** -12)
+
+
+def _row_close(got, exp, ulps=4):
+    """Normalised + rotated head rows: each element within `ulps` ulps of
+    its row's largest element.  A projected value one ulp off moves the
+    row's RMS and, through the rotation a*c - b*s, its partner element by an
+    amount set by the pair's size, not by the (possibly cancelled) result."""
+    g = np.asarray(got, np.float32)
+    e = np.asarray(exp, np.float32)
+    scale = np.max(np.abs(e), axis=-1, keepdims=True)
+    return np.all(np.abs(g - e) <= ulps * scale * 2.0 ** -10 + 2.0 ** -12)
+
+
+def test_installed_prefill_full_attention(device):
+    """_prefill_full_attention (engine.py:3043-3139) on an installed engine:
+    two full-attention layers (3 and 7), an 80-token prefill (two producer
+    launch pairs) then a 48-token chunk after it.  Per layer: Q, Q_gate and
+    the cache rows within the projection's rounding of
+    oracle.project_append on the engine's normed rows (gate and V within
+    one ulp, normalised + rotated Q and K within 4 ulps of each head row's
+    largest element); the gated attention within 2e-3 of the
+    oracle's causal attention over every row so far followed by the gate;
+    the hidden rows within one ulp of oracle.out_project plus the residual."""
+    from mi50grad_amd import attention as att
+    say("installed _prefill_full_attention")
+    rng = np.random.default_rng(81)
+    cfg = AttnConfig(num_hidden_layers=8, hidden_size=512)
+    kv = KVCache(cfg, 256, device, batch_size=1)
+    eng = att.install(StubEngine(cfg, device, kv, rng, 512))
+    assert eng._prefill_full_attention.__func__ is FullAttentionLaunchers._prefill_full_attention
+    h, q_dim = 512, H * D
+    cos, sin = orc.rope_tables(256)
+    hist = {li: ([], []) for li in kv.full_layer_indices}
+    for seq_len in (80, 48):
+        start = kv.current_len
+        pos = np.arange(start, start + seq_len)
+        eng._alloc_prefill_scratch(seq_len)
+        x0 = rng.standard_normal((seq_len, h), dtype=np.float32).astype(np.float16)
+        device.upload(eng.d_pf_hidden, x0.tobytes())
+        for li in kv.full_layer_indices:
+            w = eng.host[li]
+            before = np.frombuffer(device.download(eng.d_pf_hidden, seq_len * h * 2), np.float16).reshape(seq_len, h)
+            eng._prefill_full_attention(li, eng.layers[li], seq_len)
+            device.synchronize()
+            rd = lambda p, shape: np.frombuffer(device.download(p, int(np.prod(shape)) * 2), np.float16).reshape(shape)
+            normed = rd(eng.d_pf_normed, (seq_len, h))
+            q_o, g_o, _, k_o, v_o = orc.project_append(normed, w["wq"], w["wkv"], w["qn"], w["kn"], cos[pos], sin[pos])
+            q_g, g_g = rd(eng.d_pf_q, (seq_len, H, D)), rd(eng.d_pf_q_gate, (seq_len, H, D))
+            assert _row_close(q_g, q_o) and _ulp_close(g_g, g_o), (seq_len, li)
+            ks, vs = kv.paged.gather(kv._full_layer_slot(li), 0, start + seq_len)
+            assert _row_close(ks[start:], k_o) and _ulp_close(vs[start:], v_o), (seq_len, li)
+            hist[li][0].append(ks[start:])
+            hist[li][1].append(vs[start:])
+            kall, vall = np.concatenate(hist[li][0]), np.concatenate(hist[li][1])
+            att_o = orc.chunk_attention(q_g, kall, vall, start)
+            out_g = rd(eng.d_pf_attn_out, (seq_len, H, D))
+            assert max_err(out_g, orc.sigmoid_gate(att_o.astype(np.float16), g_g)) <= 2e-3, (seq_len, li)
+            x_exp = orc.out_project(out_g.reshape(seq_len, q_dim), w["wo"], before)
+            assert _ulp_close(rd(eng.d_pf_hidden, (seq_len, h)), x_exp), (seq_len, li)
+        kv.current_len = start + seq_len  # prefill_step's bookkeeping (engine.py:3283)
+    kv.cleanup()
+
+
+def test_decode_launch_cache_and_rollback(device):
+    """build_decode_launch_cache (engine.py:3309-3555): per step the caller
+    moves cos/sin (params 2, 3), the K slot (qknorm_k params 4) and seq_len
+    (decode_attn params 4) in place and launches with device.launch_cached,
+    V going to its slot directly (engine.py:2012-2018); outputs against the
+    oracle.  Then rollback_kv_cache(2) (tp_engine.py:1673-1687) and a step
+    that overwrites the dropped rows must see the truncated history."""
+    from mi50grad_amd import attention as att
+    say("decode launch cache + rollback_kv_cache")
+    rng = np.random.default_rng(83)
+    cfg = AttnConfig(num_hidden_layers=4, hidden_size=512)
+    kv = KVCache(cfg, 128, device, batch_size=1)
+    eng = att.install(StubEngine(cfg, device, kv, rng, 512))
+    eng.set_direct_kv_write(True)
+    lc = eng.build_decode_launch_cache()
+    assert list(lc) == [3] and {"qknorm_q", "qknorm_k", "decode_attn"} <= set(lc[3])
+    w = eng.host[3]
+    cos, sin = orc.rope_tables(128)
+    hk, hv = [], []
+    for step in range(12):
+        if step == 9:
+            eng.rollback_kv_cache(2)
+            del hk[-2:], hv[-2:]
+            assert kv.current_len == 7
+        pos = kv.current_len
+        q = rng.standard_normal((H, D)).astype(np.float16)
+        k = rng.standard_normal((HKV, D)).astype(np.float16)
+        v = rng.standard_normal((HKV, D)).astype(np.float16)
+        device.upload(eng.d_q, q.tobytes())
+        device.upload(eng.d_k, k.tobytes())
+        k_slot, v_slot = kv.get_kv_ptr(3, pos)
+        device.upload(v_slot, v.tobytes())
+        off = pos * (eng.rotary_dim // 2) * 2
+        for name in ("qknorm_q", "qknorm_k"):
+            lc[3][name].params[2].value = eng.d_cos + off
+            lc[3][name].params[3].value = eng.d_sin + off
+        lc[3]["qknorm_k"].params[4].value = k_slot
+        lc[3]["decode_attn"].params[4].value = pos + 1
+        for name in ("qknorm_q", "qknorm_k", "decode_attn"):
+            device.launch_cached(lc[3][name])
+        device.synchronize()
+        qn = orc.qknorm_rope_exact(q, w["qn"], np.repeat(cos[pos:pos + 1], H, 0), np.repeat(sin[pos:pos + 1], H, 0))
+        kn = orc.qknorm_rope_exact(k, w["kn"], np.repeat(cos[pos:pos + 1], HKV, 0), np.repeat(sin[pos:pos + 1], HKV, 0))
+        hk.append(kn)
+        hv.append(v)
+        out = np.frombuffer(device.download(eng.d_attn_out, H * D * 2), np.float16).reshape(H, D)
+        assert max_err(out, orc.attention_fp32(qn[None], np.stack(hk), np.stack(hv))[0]) <= 2e-3, step
+        kv.advance()
+    kv.cleanup()
+
+
+def test_gemv_fp16_lm_head_shape(device):
+    """_launch_gemv_fp16 with an lm_head-like output width (the reference's
+    vocab, 248320 rows) for one token: bit-exact on fp32-exact inputs."""
+    say("GEMV with vocab-wide output")
+    rng = np.random.default_rng(84)
+    cfg = AttnConfig(num_hidden_layers=4)
+    eng = FullAttentionLaunchers(cfg, device, max_seq_len=64)
+    K, N = 512, 248320
+    x = rng.integers(-3, 4, K).astype(np.float16)
+    w = (rng.integers(-2, 3, (N, K)) * 2.0 ** -7).astype(np.float16)
+    dx, dw, dy = device.array(x), device.array(w), device.empty((N,), np.float16)
+    eng._launch_gemv_fp16(dy.ptr, dx.ptr, dw.ptr, K, N)
+    device.synchronize()
+    assert np.array_equal(dy.numpy().view(np.uint16), orc.out_project(x[None], w)[0].view(np.uint16))
+    with pytest.raises(ValueError):
+        eng._launch_gemv_fp16(dy.ptr, dx.ptr, dw.ptr, 500, N)
+
+
+def test_tree_attention_mask_drives_tree_verify(device):
+    """A TreeAttentionMask (tree_attention.py:148-268) built from the
+    reference's classes gives kva_step_begin its tree bits; tree verify over
+    its topology matches the oracle's masked attention."""
+    from mi50grad_amd import tree as tr
+    from gpu_helpers import build_cache
+    say("TreeAttentionMask -> tree verify")
+    rng = np.random.default_rng(85)
+    topo = tr.build_complete_binary_tree(1000, 2)
+    par = topo.parents()
+    lengths = [300, 47]
+    T = topo.get_tree_size()
+    ids = [list(range(0, 20)), list(range(20, 24))]
+    cache, kr, vr = build_cache([L + T for L in lengths], ids, extra_rows=0, rng=rng)
+    for b, L in enumerate(lengths):
+        cache.set_len(b, L)
+    masks = [tr.TreeAttentionMask(topo, kv_len=L) for L in lengths]
+    q = rng.standard_normal((2 * T, H, D), dtype=np.float32).astype(np.float16)
+    dq, out = device.array(q), device.empty((2 * T, H, D), np.float16)
+    cache.begin_step([0, 1], [T, T], tree_bits=masks[0].tree_bits() + masks[1].tree_bits())
+    cache.tree_verify(0, dq, out)
+    device.synchronize()
+    got = out.numpy()
+    for b, L in enumerate(lengths):
+        s = slice(b * T, b * T + T)
+        exp = orc.tree_attention(q[s], kr[0][b][:L], vr[0][b][:L], kr[0][b][L:], vr[0][b][L:], par)
+        assert max_err(got[s], exp) <= 2e-3, b
+    cache.destroy()
