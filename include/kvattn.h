@@ -226,6 +226,18 @@ int kva_prefill(kva_cache *cache, int32_t layer, const void *q, void *out,
  * (tp_engine.py:3186-3214).  q, out: [T, num_heads, 256] fp16.            */
 int kva_tree_verify(kva_cache *cache, int32_t layer, const void *q, void *out,
                     kva_stream_t stream);
+/* kva_prefill / kva_tree_verify with the attention output gate fused into
+ * the epilogue, as kva_decode_gated: out = fp16(fp16(attn) * sigmoid(gate)),
+ * the _launch_sigmoid_mul(d_pf_attn_out, d_pf_q_gate, seq_len*q_dim) that
+ * follows the prefill attention at engine.py:3120-3121 (sigmoid_mul.hip:
+ * 10-22).  gate: new token t's row of num_heads*256 values at
+ * gate + t*gate_stride (num_heads*256 for the engine's d_pf_q_gate buffer,
+ * 2*num_heads*256 for the Q_gate half of a fused [Q | Q_gate] row);
+ * 8-byte aligned.                                                          */
+int kva_prefill_gated(kva_cache *cache, int32_t layer, const void *q, const void *gate,
+                      int64_t gate_stride, void *out, kva_stream_t stream);
+int kva_tree_verify_gated(kva_cache *cache, int32_t layer, const void *q, const void *gate,
+                          int64_t gate_stride, void *out, kva_stream_t stream);
 /* Keep accepted tree rows and drop the rest, in every layer: for sequence
  * seq_ids[b], rows base_len[b] + keep_rows[j] (j in [keep_off[b],
  * keep_off[b+1]), strictly increasing) move to base_len[b] + (j -

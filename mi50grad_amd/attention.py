@@ -204,13 +204,13 @@ class FullAttentionLaunchers:
         Per token the engine's RMSNorm of the hidden state (its own kernel,
         as in the reference) into d_pf_normed; then, for all tokens at once
         through libkvattn: the Q/Q_gate/K/V projection with QK-norm + RoPE and
-        the K/V append into the cache (kva_project_append) and causal
-        attention over the cache (kva_prefill); the engine's own sigmoid gate
-        on the attention rows, as the reference calls it (engine.py:3120-
-        3121); and the O-projection with the residual add into d_pf_hidden
-        (kva_out_project, one rounding after the add where the reference's
-        GEMM + residual_add round twice: the two differ by at most one fp16
-        ulp).  The chunk goes to slots [current_len,
+        the K/V append into the cache (kva_project_append), causal attention
+        over the cache with the sigmoid gate the reference applies next
+        (_launch_sigmoid_mul, engine.py:3120-3121) fused into its epilogue
+        (kva_prefill_gated, same rounding), and the O-projection with the
+        residual add into d_pf_hidden (kva_out_project, one rounding after
+        the add where the reference's GEMM + residual_add round twice: the
+        two differ by at most one fp16 ulp).  The chunk goes to slots [current_len,
         current_len + seq_len), attending causally over everything before
         it; the reference's prefill starts from an empty cache, which is the
         current_len = 0 case.  The caller sets current_len afterwards, as
@@ -230,8 +230,8 @@ class FullAttentionLaunchers:
         paged.project_append(layer, self.d_pf_normed, h, wq, wkv, lw.q_norm, lw.k_norm, self.d_cos,
                              self.d_sin, self.rope_rows, self.d_pf_q, q_gate_out=self.d_pf_q_gate,
                              stream=self._kva_stream)
-        paged.prefill(layer, self.d_pf_q, self.d_pf_attn_out, stream=self._kva_stream)
-        self._launch_sigmoid_mul(self.d_pf_attn_out, self.d_pf_q_gate, seq_len * q_dim)
+        paged.prefill(layer, self.d_pf_q, self.d_pf_attn_out, stream=self._kva_stream, gate=self.d_pf_q_gate,
+                      gate_stride=q_dim)
         paged.out_project(self.d_pf_attn_out, seq_len, q_dim, lw.o_weight, h, self.d_pf_hidden,
                           residual=self.d_pf_hidden, stream=self._kva_stream)
 

@@ -401,15 +401,14 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             if (whole) {
                 if (qvalid[t]) {
                     const float inv = 1.0f / lt;
-                    uint16_t *orow =
-                        a.out + (static_cast<size_t>(cu.tok + cu.tile * Q + iq[t]) * nh + cu.h * G + gq[t]) * kHeadDim;
+                    const size_t tq = static_cast<size_t>(cu.tok + cu.tile * Q + iq[t]);
+                    uint16_t *orow = a.out + (tq * nh + cu.h * G + gq[t]) * kHeadDim;
+                    const uint16_t *grow = a.gate ? a.gate + tq * a.gate_stride + (cu.h * G + gq[t]) * kHeadDim : nullptr;
 #pragma unroll
-                    for (int dt = 0; dt < 16; ++dt) {
-                        uint2 o;
-                        o.x = pack_h2(acc[t][dt][0] * inv, acc[t][dt][1] * inv);
-                        o.y = pack_h2(acc[t][dt][2] * inv, acc[t][dt][3] * inv);
-                        *reinterpret_cast<uint2 *>(orow + 16 * dt + 4 * grp) = o;
-                    }
+                    for (int dt = 0; dt < 16; ++dt)
+                        *reinterpret_cast<uint2 *>(orow + 16 * dt + 4 * grp) =
+                            out_fp16x4(acc[t][dt][0] * inv, acc[t][dt][1] * inv, acc[t][dt][2] * inv,
+                                       acc[t][dt][3] * inv, grow ? grow + 16 * dt + 4 * grp : nullptr);
                 }
             } else {
                 // Slot 2w: the unit began at or before this share (its first
@@ -527,18 +526,16 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
         big = nb;
     }
     const float inv = 1.0f / lt;
-    uint16_t *orow = a.out + (static_cast<size_t>(tok + qi) * a.num_heads + h * G + gq) * kHeadDim + d0;
-    uint4 o0, o1;
-    o0.x = pack_h2(o[0] * inv, o[1] * inv);
-    o0.y = pack_h2(o[2] * inv, o[3] * inv);
-    o0.z = pack_h2(o[4] * inv, o[5] * inv);
-    o0.w = pack_h2(o[6] * inv, o[7] * inv);
-    o1.x = pack_h2(o[8] * inv, o[9] * inv);
-    o1.y = pack_h2(o[10] * inv, o[11] * inv);
-    o1.z = pack_h2(o[12] * inv, o[13] * inv);
-    o1.w = pack_h2(o[14] * inv, o[15] * inv);
-    *reinterpret_cast<uint4 *>(orow) = o0;
-    *reinterpret_cast<uint4 *>(orow + 8) = o1;
+    const size_t tq = static_cast<size_t>(tok + qi);
+    uint16_t *orow = a.out + (tq * a.num_heads + h * G + gq) * kHeadDim + d0;
+    const uint16_t *grow = a.gate ? a.gate + tq * a.gate_stride + (h * G + gq) * kHeadDim + d0 : nullptr;
+    uint2 p[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        p[e] = out_fp16x4(o[4 * e] * inv, o[4 * e + 1] * inv, o[4 * e + 2] * inv, o[4 * e + 3] * inv,
+                          grow ? grow + 4 * e : nullptr);
+    *reinterpret_cast<uint4 *>(orow) = make_uint4(p[0].x, p[0].y, p[1].x, p[1].y);
+    *reinterpret_cast<uint4 *>(orow + 8) = make_uint4(p[2].x, p[2].y, p[3].x, p[3].y);
 }
 
 template <int NT, int WAVES>

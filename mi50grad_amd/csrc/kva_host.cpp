@@ -1033,7 +1033,7 @@ int kva_decode_gated(kva_cache *c, int32_t layer, const void *q, const void *gat
 }
 
 static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream,
-                       bool tree) {
+                       bool tree, const void *gate = nullptr, int64_t gate_stride = 0) {
     if (int rc = refuse_while_capturing(c, tree ? "kva_tree_verify" : "kva_prefill")) return rc;
     int rc = require_device(c);
     if (rc) return rc;
@@ -1042,8 +1042,11 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     if (tree && !c->st_has_bits) return fail(KVA_ERR_STATE, "tree verify needs tree_bits in kva_step_begin");
     if (!q || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (!aligned16(q) || !aligned16(out)) return fail(KVA_ERR_MISALIGNED, "q/out must be 16-byte aligned");
+    if ((rc = check_gate(gate, gate_stride, c->cfg.num_heads))) return rc;
     if (c->st_n_tok == 0) return KVA_OK;
     kva::MultiQueryArgs a{};
+    a.gate = static_cast<const uint16_t *>(gate);
+    a.gate_stride = gate_stride;
     a.q = static_cast<const uint16_t *>(q);
     a.out = static_cast<uint16_t *>(out);
     a.k_pool = c->d_k + c->layer_elems * layer;
@@ -1084,6 +1087,18 @@ int kva_prefill(kva_cache *c, int32_t layer, const void *q, void *out, kva_strea
 
 int kva_tree_verify(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream) {
     return multi_query(c, layer, q, out, stream, true);
+}
+
+int kva_prefill_gated(kva_cache *c, int32_t layer, const void *q, const void *gate, int64_t gate_stride,
+                      void *out, kva_stream_t stream) {
+    if (!gate) return fail(KVA_ERR_INVALID_ARG, "NULL gate");
+    return multi_query(c, layer, q, out, stream, false, gate, gate_stride);
+}
+
+int kva_tree_verify_gated(kva_cache *c, int32_t layer, const void *q, const void *gate, int64_t gate_stride,
+                          void *out, kva_stream_t stream) {
+    if (!gate) return fail(KVA_ERR_INVALID_ARG, "NULL gate");
+    return multi_query(c, layer, q, out, stream, true, gate, gate_stride);
 }
 
 int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int32_t *base_len,

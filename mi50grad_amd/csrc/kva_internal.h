@@ -202,6 +202,10 @@ struct MultiQueryArgs {
     int32_t q_tile;           // new tokens per unit tile: mq_tile_tokens(G, n_waves, n_t)
     float *ws_acc;            // [2*n_wg][kMqSlotRows][256] partial slots
     float *ws_ml;             // [2*n_wg][kMqSlotRows][2]
+    // Output gate (null = none), as in DecodeArgs: new token t's row of
+    // query head hq at gate + t*gate_stride + hq*256.
+    const uint16_t *gate;
+    int64_t gate_stride;
 };
 constexpr int kMqKeys = 32;       // keys per multi-query block
 // The stream-K split of the multi-query kernel counts each unit as this many

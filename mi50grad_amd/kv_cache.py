@@ -177,11 +177,22 @@ class PagedKVCache:
             stride = gate_stride or self.num_heads * 256
             _lib.call("kva_decode_gated", self.handle, layer, _ptr(q), _ptr(gate), stride, _ptr(out), stream)
 
-    def prefill(self, layer: int, q, out, stream=None) -> None:
-        _lib.call("kva_prefill", self.handle, layer, _ptr(q), _ptr(out), stream)
+    def prefill(self, layer: int, q, out, stream=None, gate=None, gate_stride: int = 0) -> None:
+        """Causal attention of the step's new rows; with `gate`, the output
+        gate (out *= sigmoid(gate), engine.py:3120-3121) in the same launch."""
+        if gate is None:
+            _lib.call("kva_prefill", self.handle, layer, _ptr(q), _ptr(out), stream)
+        else:
+            stride = gate_stride or self.num_heads * 256
+            _lib.call("kva_prefill_gated", self.handle, layer, _ptr(q), _ptr(gate), stride, _ptr(out), stream)
 
-    def tree_verify(self, layer: int, q, out, stream=None) -> None:
-        _lib.call("kva_tree_verify", self.handle, layer, _ptr(q), _ptr(out), stream)
+    def tree_verify(self, layer: int, q, out, stream=None, gate=None, gate_stride: int = 0) -> None:
+        if gate is None:
+            _lib.call("kva_tree_verify", self.handle, layer, _ptr(q), _ptr(out), stream)
+        else:
+            stride = gate_stride or self.num_heads * 256
+            _lib.call("kva_tree_verify_gated", self.handle, layer, _ptr(q), _ptr(gate), stride, _ptr(out),
+                      stream)
 
     def rollback(self, seq_ids: Sequence[int], base_len: Sequence[int],
                  keep_rows: Sequence[Sequence[int]], stream=None) -> None:

@@ -110,9 +110,6 @@ def _prefilled(rng, prefix, chunk):
     return cache, kr[0], vr[0]
 
 
-@pytest.mark.skip(reason="the gated multi-query epilogue (kva_prefill_gated / kva_tree_verify_gated) was "
-                         "taken out: the GPU run that first exercised its tree form ended in a GPU fault whose "
-                         "cause was not found; prefill gates through the engine's sigmoid_mul instead")
 @pytest.mark.parametrize("tree", [False, True])
 def test_multi_query_gated(device, tree):
     """kva_prefill_gated on config 4's shape (512-token chunks after 0/256/

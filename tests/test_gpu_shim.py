@@ -132,7 +132,7 @@ class StubEngine:
     InferenceEngine: config, device, kv_cache, layers with the stacked
     attention weights of engine.py:1366-1378, the decode buffers (d_q, d_k,
     d_attn_out), the prefill buffers, and the engine's own hidden-state
-    RMSNorm and sigmoid gate (outside this path; here numpy on the host)."""
+    RMSNorm (outside this path; here numpy on the host)."""
 
     _alloc_prefill_scratch = FullAttentionLaunchers._alloc_prefill_scratch
 
@@ -161,11 +161,6 @@ class StubEngine:
         self.d_q = device.malloc(q_dim * 2)
         self.d_k = device.malloc(kv_dim * 2)
         self.d_attn_out = device.malloc(q_dim * 2)
-
-    def _launch_sigmoid_mul(self, attn_out, gate, n):
-        a = np.frombuffer(self.device.download(attn_out, n * 2), np.float16)
-        g = np.frombuffer(self.device.download(gate, n * 2), np.float16)
-        self.device.upload(attn_out, orc.sigmoid_gate(a, g).tobytes())
 
     def _launch_rmsnorm(self, dst, src, weight, dim):
         x = np.frombuffer(self.device.download(src, dim * 2), np.float16).astype(np.float32)
