@@ -333,6 +333,14 @@ int kva_legacy_decode_batched(kva_cache *ws, const void *q, const void *k_base,
  * known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE counters.      */
 int kva_hbm_copy(void *dst, const void *src, size_t bytes, kva_stream_t stream);
 
+/* HBM read-only stream probe: one kernel reading `bytes` (a multiple of 16,
+ * src 16-byte aligned) with 16-byte lanes, eight loads in flight per lane;
+ * `sink` (one 4-byte word) is written only when the data's XOR fold hits a
+ * fixed value, so the reads cannot be dropped.  The read-side ceiling the
+ * decode attention is measured against; like kva_hbm_copy, the measured
+ * counterpart of the reference's bench/micro/hbm_bandwidth.hip.cpp.        */
+int kva_hbm_read(const void *src, size_t bytes, void *sink, kva_stream_t stream);
+
 /* ---- device helpers (the GPUDevice surface, hip_dispatch.py:594-703) ----- */
 int kva_dev_count(int32_t *n);
 int kva_dev_set(int32_t device);

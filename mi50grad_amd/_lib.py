@@ -88,6 +88,7 @@ SIGNATURES = {
     "kva_legacy_decode_gated": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "kva_legacy_decode_batched": [_P, _P, _P, _P, _P, _I, _I, c_int64, _I, _I, _P],
     "kva_hbm_copy": [_P, _P, c_size_t, _P],
+    "kva_hbm_read": [_P, c_size_t, _P, _P],
     "kva_dev_count": [_PI],
     "kva_dev_set": [_I],
     "kva_dev_malloc": [POINTER(c_void_p), c_size_t],

@@ -1382,6 +1382,15 @@ int kva_hbm_copy(void *dst, const void *src, size_t bytes, kva_stream_t stream) 
     return KVA_OK;
 }
 
+int kva_hbm_read(const void *src, size_t bytes, void *sink, kva_stream_t stream) {
+    if (!src || !sink) return fail(KVA_ERR_INVALID_ARG, "NULL pointer");
+    if (bytes % 16 != 0) return fail(KVA_ERR_INVALID_ARG, "bytes %zu not a multiple of 16", bytes);
+    if (!aligned16(src) || (reinterpret_cast<uintptr_t>(sink) & 3u))
+        return fail(KVA_ERR_MISALIGNED, "src must be 16-byte and sink 4-byte aligned");
+    KVA_HIP(kva::launch_read(src, bytes, static_cast<uint32_t *>(sink), static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
 // ---- device helpers -------------------------------------------------------
 int kva_dev_count(int32_t *n) {
     if (!n) return fail(KVA_ERR_INVALID_ARG, "NULL argument");

@@ -159,6 +159,9 @@ hipError_t launch_table_patch(int32_t *table, int32_t table_stride,
 
 // Streaming device copy (bytes multiple of 16): the HBM bandwidth probe.
 hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
+// Read-only stream over `bytes` (multiple of 16): the read-bandwidth probe.
+// sink: one word, written only when the data's XOR fold hits a fixed value.
+hipError_t launch_read(const void *src, size_t bytes, uint32_t *sink, hipStream_t s);
 
 // Move accepted rows of each sequence, in every layer (tree rollback).
 struct RollbackArgs {
