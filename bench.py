@@ -110,7 +110,27 @@ def make_inputs(dev: GPUDevice, n_tok: int, seed: int = 1):
     return per_layer
 
 
-def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, label):
+def timeline_summary(rec: np.ndarray) -> dict:
+    """Summary of one decode launch's timeline (kva_timeline_read records,
+    [n_wg, rows, 8 waves, 4]): per workgroup, entry = first wave's entry,
+    first issue = when its first K/V loads were out, end = its last wave's
+    walk end; microseconds (100 MHz ticks)."""
+    ent = rec[:, :, :, 0].min(axis=(1, 2))
+    first = rec[:, :, :, 1].max(axis=(1, 2))
+    end = rec[:, :, :, 2].max(axis=(1, 2))
+    xcd = (rec[:, 0, 0, 3] >> 32) & 0xF
+    t0 = ent.min()
+    dur = (end - ent) / 100.0
+    return {"workgroups": int(rec.shape[0]), "entry_spread_us": float((ent.max() - t0) / 100.0),
+            "first_issue_us": {"median": float(np.median((first - ent) / 100.0)),
+                               "max": float(((first - ent) / 100.0).max())},
+            "wg_duration_us": {"min": float(dur.min()), "median": float(np.median(dur)), "max": float(dur.max())},
+            "span_us": float((end.max() - t0) / 100.0),
+            "xcd_mean_duration_us": [round(float(dur[xcd == x].mean()), 2) if (xcd == x).any() else None
+                                     for x in range(8)]}
+
+
+def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, label, timeline=False):
     B = len(lengths)
     mbps = max(len(ids) for ids in block_ids)
     cache = PagedKVCache(n_layers=LAYERS, max_seqs=B, max_blocks=n_blocks, max_blocks_per_seq=mbps,
@@ -157,6 +177,28 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
             a.destroy()
             b.destroy()
     log(f"{label}: {steps} steps in {wall * 1e3:.2f} ms; decode kernel avg {np.mean(dec_ms) * 1e3:.1f} us")
+    tl = None
+    if timeline:
+        # Outside the timed region: one more step, each layer's decode
+        # followed by a read of its timeline (the read synchronises).
+        cache.timeline_enable(True)
+        for b in seqs:
+            cache.set_len(b, int(lengths[b]))
+        cache.begin_step(seqs, ones)
+        samples = []
+        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
+            cache.decode(layer, q, out)
+            samples.append(timeline_summary(cache.timeline()))
+        cache.timeline_enable(False)
+        med = lambda f: float(np.median([f(x) for x in samples]))
+        tl = {"launches": len(samples),
+              "first_issue_us_median": med(lambda x: x["first_issue_us"]["median"]),
+              "wg_duration_us_median": med(lambda x: x["wg_duration_us"]["median"]),
+              "wg_duration_us_max": med(lambda x: x["wg_duration_us"]["max"]),
+              "span_us": med(lambda x: x["span_us"]),
+              "xcd_mean_duration_us": [round(med(lambda x, i=i: x["xcd_mean_duration_us"][i]), 2) for i in range(8)],
+              "per_launch": samples}
     cache.destroy()
     ctx = np.asarray(lengths, dtype=np.int64) + 1
     by = wl.decode_bytes(ctx)
@@ -165,7 +207,7 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
         "kv_bytes_per_layer": by["kv"], "alg_bytes_decode_launch": by["kv"] + by["q"],
         "alg_bytes_layer_step": by["kv"] + by["q"] + by["out"] + by["append"],
         "decode_avg_us": float(np.mean(dec_ms) * 1e3), "decode_min_us": float(np.min(dec_ms) * 1e3),
-        "split_tokens": split_used, "n_splits": n_splits,
+        "split_tokens": split_used, "n_splits": n_splits, "timeline": tl,
     }
 
 
@@ -688,6 +730,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="c3: leave out the ctx8192 variant and the bandwidth probes")
+    ap.add_argument("--timeline", action="store_true",
+                    help="c3/ctx8192: after the timed steps, record the decode kernels' per-workgroup "
+                         "timeline (kva_timeline_enable) for one more step and add its summary")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build runs the path on a single MI355X "
@@ -802,7 +847,7 @@ def main() -> int:
             "vendor_hbm_gbs": HBM_PEAK_GBS,
             "measured_stream_read_gbs": rd["gbs"], "measured_stream_copy_gbs": cp["gbs"],
             "decode_frac_of_measured_read": line["roofline"]["achieved"] / rd["gbs"],
-            "method": "kva_hbm_read over 4 GiB (read-only, 8 x 16-byte loads in flight per lane) and "
+            "method": "kva_hbm_read over 4 GiB (read-only: 2048 contiguous shares, two passes of 4 x 16-byte loads per lane in flight) and "
                       "kva_hbm_copy over 4 GiB (bytes read + written), averages of 20 launches between "
                       "HIP events; roofline.frac stays against the vendor 8 TB/s"}
     if not args.no_cpu_baseline:
@@ -828,7 +873,8 @@ def decode_line(dev, which, args):
         nb = 32 * nblk
         workload = ("C3 at fixed ctx: B=32, every sequence 8192 cached rows, append 1 then attend over "
                     "8193; 16 layers, 24 q / 4 kv heads, d=256, fp16 16-token pages, permuted ids")
-    r = decode_workload(dev, lengths, ids, nb, args.steps, args.warmup, args.split, which)
+    r = decode_workload(dev, lengths, ids, nb, args.steps, args.warmup, args.split, which,
+                        timeline=getattr(args, "timeline", False))
     kv_total = r["kv_bytes_per_layer"] * LAYERS * r["steps"]
     value = kv_total / r["wall_s"] / 1e9
     ms_step = r["wall_s"] * 1e3 / r["steps"]
@@ -844,6 +890,7 @@ def decode_line(dev, which, args):
                    "flush": "none: each layer-step reads its own layer's pages, 0.6-1.1 GB, past the 256 MB MALL"},
         "pct_of_hbm_peak": 100.0 * value / HBM_PEAK_GBS,
         "tok_per_s": r["B"] * r["steps"] / r["wall_s"],
+        **({"timeline": r["timeline"]} if r["timeline"] else {}),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": load_traffic(traffic_file),

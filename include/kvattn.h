@@ -254,6 +254,20 @@ int kva_set_decode_split(kva_cache *cache, int32_t split_tokens);
 int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,
                          int32_t *n_splits);
 
+/* Decode timeline (no counterpart in the reference, which has no tracer:
+ * its timing is perf_counter around a device sync, bench_optimization_
+ * baseline.py:54-69).  While enabled, every kva_decode on this cache records
+ * per wave, in the kernel itself: its workgroup's entry time, the time the
+ * first K/V loads were issued, the end of its page walk (100 MHz ticks of the
+ * GPU's constant clock), and the XCD (bits 32-35) with the workgroup's page
+ * count (bits 0-31).  kva_timeline_read copies the last decode's records,
+ * [n_wg][grid_rows][8 waves][4] words (a synchronising call); the recorded
+ * workload is otherwise unchanged.  Off by default; costs one device buffer
+ * while on.                                                                 */
+int kva_timeline_enable(kva_cache *cache, int32_t on);
+int kva_timeline_read(const kva_cache *cache, uint64_t *dst, size_t cap_words,
+                      int32_t *n_wg, int32_t *grid_rows);
+
 /* ---- recorded steps (hipGraph replay) ------------------------------------ */
 /* Replaces the per-step kernel-node patching of the reference's graph
  * dispatch (c_graph_dispatch.c:392-414 update_mutable_params, which rewrote

@@ -310,6 +310,10 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
     // Wave 2h+1's state for wave 2h to merge at a sequence end.
     __shared__ float4 mrg_acc[kDecodeHeadsPerWg * G * 64];
     __shared__ float mrg_ml[kDecodeHeadsPerWg * G * 2];
+    // Timeline (a.timeline set): entry and first-issue times, kept in LDS so
+    // they hold no registers across the walk.
+    __shared__ uint64_t tl_t[2];
+    if (a.timeline && threadIdx.x == 0) tl_t[0] = __builtin_amdgcn_s_memrealtime();
 
     const int w = blockIdx.x;
     int P, W;
@@ -510,6 +514,7 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
         }
         id_last = cq[kStages - 1].ok ? page_id(cq[kStages - 1]) : id;
     }
+    if (a.timeline && threadIdx.x == 0) tl_t[1] = __builtin_amdgcn_s_memrealtime();
     // One step: issue cq[last] into `nr`, fold cq[0] (in `cr`) in, finish the
     // sequence when the next page belongs to another one.
     auto step = [&](HalfPage &cr, HalfPage &nr) -> bool {
@@ -542,6 +547,17 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
     } else {
         while (step(A, B) && step(B, A)) {
         }
+    }
+    if (a.timeline && lane == 0) {
+        // Per wave: entry, first K/V issue, end of its walk (100 MHz
+        // s_memrealtime ticks), then the XCD (high word) and the range's pages.
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        uint64_t *rec = a.timeline + ((static_cast<size_t>(w) * gridDim.y + blockIdx.y) * 8 + wave) * kTimelineWords;
+        rec[0] = tl_t[0];
+        rec[1] = tl_t[1];
+        rec[2] = __builtin_amdgcn_s_memrealtime();
+        rec[3] = (static_cast<uint64_t>(xcc & 0xf) << 32) | static_cast<uint32_t>(p_end - p_begin);
     }
 }
 

@@ -72,6 +72,7 @@ struct kva_cache {
     size_t aux_bytes = 0;
     float *d_ws_acc = nullptr;
     float *d_ws_ml = nullptr;
+    uint64_t *d_timeline = nullptr;  // decode timeline records (kva_timeline_enable)
     float *d_mq_acc = nullptr;  // multi-query partial slots [2*mq_max_wg][8][16][256]
     float *d_mq_ml = nullptr;
     int32_t mq_max_wg = 0;
@@ -414,6 +415,7 @@ int kva_destroy(kva_cache *c) {
         (void)hipFree(c->d_aux);
         (void)hipFree(c->d_ws_acc);
         (void)hipFree(c->d_ws_ml);
+        (void)hipFree(c->d_timeline);
         (void)hipFree(c->d_mq_acc);
         (void)hipFree(c->d_mq_ml);
         (void)hipFree(c->d_proj);
@@ -874,6 +876,45 @@ int kva_set_decode_split(kva_cache *c, int32_t split_tokens) {
     return KVA_OK;
 }
 
+// Timeline records: every decode workgroup the workspace can serve, times the
+// grid rows of a cache's own heads, eight waves each.
+static size_t timeline_words(const kva_cache *c) {
+    const int32_t hpw = std::min(c->cfg.num_kv_heads, static_cast<int32_t>(kva::kDecodeHeadsPerWg));
+    int32_t h = hpw;
+    while (c->cfg.num_kv_heads % h) --h;
+    return static_cast<size_t>(c->max_wg) * (c->cfg.num_kv_heads / h) * 8 * kva::kTimelineWords;
+}
+
+int kva_timeline_enable(kva_cache *c, int32_t on) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if (int rc = require_device(c)) return rc;
+    if (int rc = refuse_while_capturing(c, "kva_timeline_enable")) return rc;
+    if (!on) {
+        if (c->d_timeline) KVA_HIP(hipFree(c->d_timeline));
+        c->d_timeline = nullptr;
+        return KVA_OK;
+    }
+    if (c->d_timeline) return KVA_OK;
+    const size_t bytes = timeline_words(c) * sizeof(uint64_t);
+    KVA_HIP(hipMalloc(&c->d_timeline, bytes));
+    KVA_HIP(hipMemset(c->d_timeline, 0, bytes));
+    return KVA_OK;
+}
+
+int kva_timeline_read(const kva_cache *c, uint64_t *dst, size_t cap_words, int32_t *n_wg, int32_t *grid_rows) {
+    if (!c || !dst || !n_wg || !grid_rows) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    if (!c->d_timeline) return fail(KVA_ERR_STATE, "timeline not enabled (kva_timeline_enable)");
+    int32_t h = std::min(c->cfg.num_kv_heads, static_cast<int32_t>(kva::kDecodeHeadsPerWg));
+    while (c->cfg.num_kv_heads % h) --h;
+    *n_wg = c->last_nwg;
+    *grid_rows = c->cfg.num_kv_heads / h;
+    const size_t words = static_cast<size_t>(c->last_nwg) * *grid_rows * 8 * kva::kTimelineWords;
+    if (cap_words < words) return fail(KVA_ERR_CAPACITY, "timeline needs %zu words, %zu given", words, cap_words);
+    KVA_HIP(hipDeviceSynchronize());
+    KVA_HIP(hipMemcpy(dst, c->d_timeline, words * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    return KVA_OK;
+}
+
 int kva_get_decode_split(const kva_cache *c, int32_t *split_tokens, int32_t *n_splits) {
     if (!c || !split_tokens || !n_splits) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
     *split_tokens = c->last_split;
@@ -889,6 +930,7 @@ static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_
     a.n_wg = static_cast<int32_t>(std::max<int64_t>(1, std::min<int64_t>(choose_wg(c, pages), fit)));
     a.ws_acc = c->d_ws_acc;
     a.ws_ml = c->d_ws_ml;
+    a.timeline = c->d_timeline;
     c->last_nwg = a.n_wg;
     c->last_split = static_cast<int32_t>((pages * kva::kBlockTokens + a.n_wg - 1) / a.n_wg);
 }

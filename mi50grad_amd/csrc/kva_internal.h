@@ -141,7 +141,11 @@ struct DecodeArgs {
     // gate row of sequence b, query head hq at gate + b*gate_stride + hq*256.
     const uint16_t *gate;
     int64_t gate_stride;
+    // Per-workgroup timeline (null = off): record kTimelineWords words per
+    // wave, [n_wg][grid rows][8 waves], see kva_timeline_read.
+    uint64_t *timeline;
 };
+constexpr int kTimelineWords = 4;
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
 
 // Static device scratch of kva_legacy_decode_noalloc (k_noalloc.hip): the

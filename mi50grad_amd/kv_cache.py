@@ -219,6 +219,20 @@ class PagedKVCache:
         _lib.call("kva_get_decode_split", self.handle, ctypes.byref(s), ctypes.byref(n))
         return s.value, n.value
 
+    def timeline_enable(self, on: bool = True) -> None:
+        """Record per-wave timestamps in every decode launch (kva_timeline_enable)."""
+        _lib.call("kva_timeline_enable", self.handle, 1 if on else 0)
+
+    def timeline(self) -> np.ndarray:
+        """The last decode's records: int64 [n_wg, grid_rows, 8 waves, 4]
+        (entry, first K/V issue, walk end in 100 MHz ticks; XCD << 32 | pages)."""
+        n_wg, rows = ctypes.c_int32(), ctypes.c_int32()
+        cap = 1 << 22
+        buf = (ctypes.c_uint64 * cap)()
+        _lib.call("kva_timeline_read", self.handle, buf, cap, ctypes.byref(n_wg), ctypes.byref(rows))
+        words = n_wg.value * rows.value * 8 * 4
+        return np.frombuffer(buf, dtype=np.uint64, count=words).astype(np.int64).reshape(n_wg.value, rows.value, 8, 4)
+
 
 class KVCache:
     """Drop-in for the reference ``KVCache`` (engine.py:79-291).
