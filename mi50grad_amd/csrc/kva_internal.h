@@ -218,8 +218,11 @@ constexpr int kMqKeys = 32;       // keys per multi-query block
 // The stream-K split of the multi-query kernel counts each unit as this many
 // blocks more than it has (the cost of starting a unit: its query rows,
 // its output), so a share full of short units gets fewer blocks.  Unit u's
-// blocks sit at positions [mq_pre[u] + kMqUnitCost, mq_pre[u+1]).
-constexpr int kMqUnitCost = 2;
+// blocks sit at positions [mq_pre[u] + kMqUnitCost, mq_pre[u+1]).  Four:
+// a unit start measured about two blocks' time, but with two the shares
+// holding many short units still ended last (config 4: 2 -> 132 us, 3 -> 122,
+// 4 -> 116, 5 and 6 -> 116-117).
+constexpr int kMqUnitCost = 4;
 constexpr int kMqMaxGroup = 8;    // largest GQA group of the multi-query kernel
 constexpr int kMqSlotRows = 128;  // query rows of a partial slot (waves x 16 x tiles at most)
 // A unit's query rows are (token, head) pairs of the GQA group, 16 per
