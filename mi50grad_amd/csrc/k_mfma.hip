@@ -61,13 +61,21 @@ __device__ __forceinline__ int mq_wg_of(int p, int n, int W) {
     while (w + 1 < W && mq_wg_start(w + 1, n, W) <= p) ++w;
     return w;
 }
-// Largest i in [0, n) with pre[i] <= x (pre non-decreasing, pre[0] <= x);
-// wave-uniform arguments, scalar loads.
-__device__ __forceinline__ int upper_index(const int32_t *pre, int n, int x) {
-    int lo = 0, hi = n - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (ld_uniform(pre + mid) <= x) lo = mid; else hi = mid - 1;
+// Largest i in [0, n) with pre[i] <= x (pre non-decreasing, pre[0] <= x;
+// wave-uniform arguments).  Each round reads 64 evenly spaced entries of the
+// remaining interval with one vector load and keeps the stretch between the
+// last entry <= x and the next (a ballot: the entries <= x are a prefix of
+// the lanes): two rounds up to 4096 entries, where a binary search by
+// scalar loads took one dependent round trip per halving.
+__device__ __forceinline__ int upper_index(const int32_t *pre, int n, int x, int lane) {
+    int lo = 0, hi = n;  // the answer lies in [lo, hi)
+    while (hi - lo > 1) {
+        const int step = (hi - lo + 63) >> 6;  // entries between probes
+        const int i = lo + lane * step;
+        const uint64_t ok = __ballot(i < hi && pre[i] <= x);  // lane 0: pre[lo] <= x
+        const int k = ok ? 63 - __clzll(ok) : 0;
+        lo = __builtin_amdgcn_readfirstlane(lo + k * step);
+        hi = __builtin_amdgcn_readfirstlane(min(hi, lo + step));
     }
     return lo;
 }
@@ -204,9 +212,9 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
 
     // Issue side: the unit and block of the next load, kRing-1 blocks ahead
     // of the compute side, across unit boundaries.
-    const int u0 = upper_index(a.mq_pre, a.n_units, q0);
+    const int u0 = upper_index(a.mq_pre, a.n_units, q0, lane);
     const int U1 = ld_uniform(a.upre + a.n_seqs);
-    Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0 % U1));
+    Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0 % U1, lane));
     int ig = max(q0, iu.ub);
     if (ig >= q1) return;  // the share holds only a unit's start cost
     int ipage = 0;  // page of the next issue
