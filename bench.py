@@ -295,6 +295,71 @@ def proj_workload(dev, steps, warmup, hidden=5120):
             "alg_bytes_out": alg_out}
 
 
+def proj_prefill_workload(dev, steps, warmup, hidden=5120):
+    """The config-4 step's producer: kva_project_append of the 2048 new
+    tokens (4 sequences x 512 after 0/256/1024/2048 cached rows) from hidden
+    5120, with norm + RoPE + append, per layer (16 layers, own weights)."""
+    prefix, chunk = list(wl.C4_PREFIX), [wl.C4_CHUNK] * 4
+    B, T = 4, sum(chunk)
+    nblk = [(p + c + 15) // 16 for p, c in zip(prefix, chunk)]
+    cache = PagedKVCache(n_layers=LAYERS, max_seqs=B, max_blocks=sum(nblk), max_blocks_per_seq=max(nblk),
+                         max_step_tokens=T)
+    o = 0
+    for b, n in enumerate(nblk):
+        cache.set_blocks(b, list(range(o, o + n)))
+        o += n
+    cache.sync_tables()
+    cos, sin = rope_tables(4096)
+    d_cos, d_sin = dev.array(cos), dev.array(sin)
+    rng = np.random.default_rng(6)
+    tile = (rng.standard_normal(16 * 1024 * 1024, dtype=np.float32) / np.sqrt(hidden)).astype(np.float16)
+    d_tile = dev.array(tile)
+    nq, nkv = 2 * H * D * hidden * 2, 2 * HKV * D * hidden * 2
+    layers = []
+    for layer in range(LAYERS):
+        w = []
+        for nbytes in (nq, nkv):
+            d = dev.empty((nbytes // 2,), np.float16)
+            off = 0
+            while off < nbytes:
+                n = min(tile.nbytes - 4096 * layer, nbytes - off)
+                _lib.call("kva_memcpy_d2d", d.ptr + off, d_tile.ptr + 4096 * layer, n)
+                off += n
+            w.append(d)
+        qw, kw = dev.array(wl.norm_weight(rng)), dev.array(wl.norm_weight(rng))
+        layers.append((w[0], w[1], qw, kw))
+    d_tile.free()
+    x = dev.array(wl.normal_f16(rng, (T, hidden)))
+    q, g = dev.empty((T, H, D), np.float16), dev.empty((T, H, D), np.float16)
+    seqs = list(range(B))
+
+    def step(evs=None):
+        for b in seqs:
+            cache.set_len(b, prefix[b])
+        cache.begin_step(seqs, chunk)
+        for layer, (wq, wkv, qw, kw) in enumerate(layers):
+            if evs is not None:
+                evs[layer][0].record()
+            cache.project_append(layer, x, hidden, wq, wkv, qw, kw, d_cos, d_sin, 4096, q, g)
+            if evs is not None:
+                evs[layer][1].record()
+
+    for _ in range(warmup):
+        step()
+    dev.synchronize()
+    evs = [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    dev.synchronize()
+    wall = time.perf_counter() - t0
+    ms = [e[0].elapsed_ms(e[1]) for s_ in evs for e in s_]
+    path = cache.project_path()
+    cache.destroy()
+    return {"wall_s": wall, "steps": steps, "tokens": T, "hidden": hidden, "weight_bytes": nq + nkv,
+            "flops": T * (nq + nkv), "proj_avg_us": float(np.mean(ms) * 1e3), "path": path}
+
+
 def _cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -725,7 +790,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "copy", "read"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "proj4", "copy", "read"])
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
@@ -799,6 +864,23 @@ def main() -> int:
                          "kernel": "kva_project_append = proj_lds_kernel<2 token tiles, 8 waves, 7 row tiles, "
                                    "10 k-steps, 6 stages> + proj_finish_kernel",
                          "avg_us": r["proj_avg_us"], "alg_bytes_per_launch": r["alg_bytes_proj"]}}))
+        return 0
+    if args.workload == "proj4":
+        r = proj_prefill_workload(dev, args.steps, args.warmup)
+        us = r["proj_avg_us"]
+        tflops = r["flops"] / (us * 1e-6) / 1e12
+        alg = r["weight_bytes"] + r["tokens"] * r["hidden"] * 2 + 2 * r["tokens"] * (H + HKV) * D * 2
+        print(json.dumps({
+            "metric": "config-4 producer: kva_project_append of 2048 tokens from hidden 5120 (norm + RoPE + append)",
+            "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
+            "ms_per_step": r["wall_s"] * 1e3 / r["steps"], "higher_is_better": True, "dtype": "f16",
+            "data": "synthetic", "config": {"workload": "C4 producer", "layers": LAYERS, "tokens": r["tokens"],
+                                            "hidden": r["hidden"]},
+            "path": r["path"], "avg_us_per_layer": us, "weight_bytes": r["weight_bytes"],
+            "alg_bytes_per_layer": alg, "weights_gbs": r["weight_bytes"] / (us * 1e-6) / 1e9,
+            "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("project_c4_traffic.json"),
+                         "avg_us": us, "alg_flops_per_launch": r["flops"]}}))
         return 0
     if args.workload == "c4":
         r = c4_workload(dev, args.steps, args.warmup)

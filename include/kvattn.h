@@ -180,6 +180,19 @@ int kva_project_append(kva_cache *cache, int32_t layer, const void *x, int32_t h
                        const void *q_norm_w, const void *k_norm_w,
                        const void *cos_tab, const void *sin_tab, int32_t table_rows,
                        void *q_out, void *q_gate_out, void *kv_out, kva_stream_t stream);
+/* How the last kva_project_append on this cache projected: steps of up to
+ * 64 tokens through libkvattn's projection kernels (the weights are read
+ * once per 64 tokens); larger steps through one hipBLASLt GEMM per weight
+ * matrix over up to 2048 tokens (the reference's batched prefill GEMMs,
+ * engine.py:3051-3068), then the same finish kernel (fp16 rounding, norm,
+ * RoPE, append).  A larger step goes through the projection kernels when
+ * the GEMM cannot be set up (first call while a graph is being recorded,
+ * no device memory for its 64 MB workspace and 2048-token output, or no
+ * library solution for the shape): the results satisfy the same contract
+ * either way; this says which ran.                                         */
+#define KVA_PROJECT_KERNELS 0
+#define KVA_PROJECT_LIBRARY_GEMM 1
+int kva_get_project_path(const kva_cache *cache, int32_t *path);
 /* Output projection of the (gated) attention rows, the consumer of
  * kva_decode_gated: out[t] = fp16(attn[t] . W_o^T + residual[t]) for
  * t < n_tok, accumulated in fp32 and rounded once after the residual add.

@@ -79,6 +79,7 @@ SIGNATURES = {
     "kva_set_decode_split": [_P, _I],
     "kva_get_decode_split": [_P, _PI, _PI],
     "kva_timeline_enable": [_P, _I],
+    "kva_get_project_path": [_P, _PI],
     "kva_timeline_read": [_P, POINTER(c_uint64), c_size_t, _PI, _PI],
     "kva_graph_capture_begin": [_P, _P],
     "kva_graph_capture_end": [_P, _P, POINTER(c_void_p)],

@@ -434,6 +434,13 @@ hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+hipError_t launch_project_finish(const ProjectArgs &a, hipStream_t s) {
+    if (a.n_tok <= 0) return hipSuccess;
+    const int blocks_per_tok = (2 * a.num_heads + 2 * a.num_kv_heads + 7) / 8;
+    hipLaunchKernelGGL(proj_finish_kernel, dim3(a.n_tok * blocks_per_tok), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_out_project(const ProjectArgs &a, hipStream_t s) {
     if (a.n_tok <= 0) return hipSuccess;
     if (a.n_b != 0 || a.n_a % 16 != 0) return hipErrorInvalidValue;

@@ -93,6 +93,9 @@ struct ProjectArgs {
     const uint16_t *residual;
 };
 hipError_t launch_project(const ProjectArgs &a, hipStream_t s);
+// The finish kernel alone, over a.n_tok tokens of a.part (splits partials
+// [splits][n_tok][n_a + n_b] fp32): a prefill-sized step's GEMM output.
+hipError_t launch_project_finish(const ProjectArgs &a, hipStream_t s);
 hipError_t launch_out_project(const ProjectArgs &a, hipStream_t s);
 
 // Reference-compatible norm+RoPE on a contiguous [n_heads][head_dim] buffer.

@@ -159,6 +159,14 @@ class PagedKVCache:
                   _ptr(w_kv_fused), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab),
                   table_rows, _ptr(q_out), _ptr(q_gate_out), _ptr(kv_out), stream)
 
+    def project_path(self) -> str:
+        """Which path the last project_append took: "kernels" (libkvattn's
+        projection kernels, 64 tokens per launch pair) or "library_gemm"
+        (one hipBLASLt GEMM per weight matrix over up to 2048 tokens)."""
+        p = ctypes.c_int32()
+        _lib.call("kva_get_project_path", self.handle, ctypes.byref(p))
+        return {0: "kernels", 1: "library_gemm"}[p.value]
+
     def out_project(self, attn, n_tok: int, q_dim: int, w_o, n_out: int, out, residual=None,
                     stream=None) -> None:
         """O-projection of n_tok attention rows: out = fp16(attn . w_o^T +
