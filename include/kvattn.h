@@ -262,7 +262,12 @@ int kva_rollback(kva_cache *cache, int32_t n_seqs, const int32_t *seq_ids,
                  const int32_t *keep_rows, kva_stream_t stream);
 
 /* Split-K tuning for kva_decode: tokens per split (multiple of 16); 0 =
- * automatic.  Returns the value in effect through *effective.             */
+ * automatic.  Automatic runs a step whose longest sequence is at most 512
+ * rows in the whole-sequence form (each sequence walked whole by workgroups
+ * that split its kv heads' query-head groups among them, no partials, no
+ * combine launch; kva_get_decode_split then reports split 0 and the
+ * workgroup count) and longer steps stream-K over all CUs.  A nonzero split
+ * always runs stream-K.                                                     */
 int kva_set_decode_split(kva_cache *cache, int32_t split_tokens);
 int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,
                          int32_t *n_splits);
@@ -275,7 +280,9 @@ int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,
  * GPU's constant clock), and the XCD (bits 32-35) with the workgroup's page
  * count (bits 0-31).  kva_timeline_read copies the last decode's records,
  * [n_wg][grid_rows][8 waves][4] words (a synchronising call); the recorded
- * workload is otherwise unchanged.  Off by default; costs one device buffer
+ * workload is otherwise unchanged.  A decode in the whole-sequence form
+ * records its workgroups (n_wg of them, grid_rows = 1; several per sequence
+ * and kv head), each with its sequence's page count.  Off by default; costs one device buffer
  * while on.                                                                 */
 int kva_timeline_enable(kva_cache *cache, int32_t on);
 int kva_timeline_read(const kva_cache *cache, uint64_t *dst, size_t cap_words,
@@ -318,9 +325,9 @@ int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row,
 /* flash_attn_256_decode semantics (flash_attn_256_tuned.hip:198-350) on a
  * contiguous cache K/V [kv_seq_len, num_kv_heads, 256]: one query row
  * q [num_heads, 256] -> out [num_heads, 256].  `ws` (nullable) lends its
- * split-K workspace; with NULL the call runs one workgroup per sequence (one
- * CU: meant for short caches; long ones take a workspace or
- * kva_legacy_decode_noalloc).                                              */
+ * split-K workspace and split setting; with NULL the call runs the
+ * whole-sequence form at every length (one workgroup per kv head: meant for
+ * short caches; long ones take a workspace or kva_legacy_decode_noalloc).  */
 int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base,
                       const void *v_base, void *out, int32_t kv_seq_len,
                       int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream);

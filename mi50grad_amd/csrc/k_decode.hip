@@ -638,6 +638,170 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
         out_fp16x4(at.x * inv, at.y * inv, at.z * inv, at.w * inv, gate_of(a, b, h * G + g, lane));
 }
 
+// Whole-sequence decode for steps of short sequences: a workgroup walks one
+// sequence for one kv head alone, its eight waves taking half pages w, w+8,
+// w+16, ... (8 token rows each, up to three in flight per wave); the waves
+// merge through LDS and write the output.  No partials and no combine
+// launch: a step of a few pages per sequence is bound by its launches, its
+// memory round trips and the VALU work of each CU, not by bandwidth.  The
+// G query heads of a kv head are split among a.whole workgroups of GP heads
+// each (GP = G / a.whole), so a step of few sequences still spreads its
+// arithmetic over many CUs; workgroup w serves unit u = (sequence, kv head)
+// and head group z with w % 8 == u % 8, so the groups of one unit run on one
+// XCD and their reads of its K/V after the first come from that XCD's L2.
+// Correct for any length (a recorded launch keeps this form when the lengths
+// grow), fast while every sequence is a few hundred rows.
+template <int GP>
+__global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
+    __shared__ uint4 q_lds[GP * 32];
+    __shared__ uint32_t p_lds[kWholeWaves * 32];
+    __shared__ float4 mrg_acc[kWholeWaves * GP * 64];
+    __shared__ float mrg_ml[kWholeWaves * GP * 2];
+    __shared__ uint64_t tl_t[2];  // timeline: entry and first-issue times
+    if (a.timeline && threadIdx.x == 0) tl_t[0] = __builtin_amdgcn_s_memrealtime();
+    const int hkv = a.num_kv_heads;
+    const int nh = a.num_heads;
+    const int n_grp = a.whole;
+    const int w = blockIdx.x;
+    const int rest = w >> 3;
+    const int z = rest % n_grp;
+    const int u = (rest / n_grp) * 8 + (w & 7);
+    if (u >= a.n_seqs * hkv) return;  // the grid rounds the units up to 8
+    const int b = u / hkv;
+    const int h = u - b * hkv;
+    const int hq0 = h * (nh / hkv) + z * GP;  // this workgroup's first query head
+    // The length and the cache slot are requested together (no branch on the
+    // length between them); an empty sequence walks nothing and writes no
+    // output.
+    const int ctx = a.ctx_lens ? ld_uniform(a.ctx_lens + b) : a.ctx_len_const;
+    const int sid = a.table ? ld_uniform(a.seq_ids + b) : 0;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane >> 4;
+    const int j = lane & 15;
+    const int row_bytes = hkv * kHeadDim * 2;
+    const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
+    const size_t seq_ofs = a.table ? 0 : static_cast<size_t>(b) * a.seq_stride * 2;
+    const char *kpool = reinterpret_cast<const char *>(a.k_pool) + seq_ofs + h * kHeadDim * 2;
+    const char *vpool = reinterpret_cast<const char *>(a.v_pool) + seq_ofs + h * kHeadDim * 2;
+    // Page ids of the sequence's first 64 pages, lane k holding page k's.
+    const int32_t *row = a.table ? a.table + static_cast<size_t>(sid) * a.table_stride : nullptr;
+    const int npg = (max(ctx, 0) + kBlockTokens - 1) / kBlockTokens;
+    const int ids = (row && lane < npg) ? row[lane] : 0;
+    // The GP query rows, requested before the first K/V loads.
+    const int qi = threadIdx.x;
+    uint4 qin = make_uint4(0, 0, 0, 0);
+    if (qi < GP * 32) qin = ld16(a.q + (static_cast<size_t>(b) * nh + hq0) * kHeadDim + 8 * qi);
+
+    const int n_hp = (max(ctx, 0) + kHalf - 1) / kHalf;
+    const int n_i = wave < n_hp ? (n_hp - wave + kWholeWaves - 1) / kWholeWaves : 0;
+    const uint32_t koff = r * row_bytes + 16 * j;
+    const uint32_t voff = 8 * lane;
+    // Issue this wave's i-th half page into p (a no-op load past the list).
+    auto issue = [&](HalfPage &p, int i) {
+        const bool on = i < n_i;
+        const int hp = on ? wave + kWholeWaves * i : 0;
+        const int pg = hp >> 1;
+        int id = pg;
+        if (row) id = pg < 64 ? __builtin_amdgcn_readlane(ids, pg) : ld_uniform(row + pg);
+        const size_t ofs = static_cast<size_t>(id) * page_bytes + static_cast<size_t>(hp & 1) * kHalf * row_bytes;
+        load_half(p, kpool + ofs, vpool + ofs, min(kHalf, ctx - hp * kHalf), on, koff, voff, row_bytes);
+    };
+    constexpr int kStages = GP <= 6 ? 3 : 2;
+    HalfPage A, B, C;
+    issue(A, 0);
+    if (kStages == 3) issue(B, 1);
+    if (a.timeline && threadIdx.x == 0) tl_t[1] = __builtin_amdgcn_s_memrealtime();
+    if (qi < GP * 32) q_lds[qi] = qin;
+    __syncthreads();
+    uint4 qv[GP][2];
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+        qv[g][0] = q_lds[g * 32 + j];
+        qv[g][1] = q_lds[g * 32 + 16 + j];
+    }
+
+    WaveState<GP> st;
+    reset(st);
+    int i = 0;  // the half page folded in next
+    auto step = [&](HalfPage &cr, HalfPage &nr) -> bool {
+        issue(nr, i + kStages - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < n_i) {
+            compute_half<GP>(st, cr, qv, r, j, min(kHalf, ctx - (wave + kWholeWaves * i) * kHalf),
+                             p_lds + 32 * wave);
+        } else {
+            consume(cr);
+        }
+        ++i;
+        return i < n_i;
+    };
+    if constexpr (kStages == 3) {
+        while (step(A, C) && step(B, A) && step(C, B)) {
+        }
+    } else {
+        while (step(A, B) && step(B, A)) {
+        }
+    }
+    if (a.timeline && lane == 0) {
+        // As decode_kernel's records, one row per workgroup of unit u's
+        // group z: [n_units * n_grp][1][8 waves].
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        uint64_t *rec =
+            a.timeline + ((static_cast<size_t>(u) * n_grp + z) * kWholeWaves + wave) * kTimelineWords;
+        rec[0] = tl_t[0];
+        rec[1] = tl_t[1];
+        rec[2] = __builtin_amdgcn_s_memrealtime();
+        rec[3] = (static_cast<uint64_t>(xcc & 0xf) << 32) | static_cast<uint32_t>(npg);
+    }
+
+    // Merge the eight waves: each leaves (m, l, acc) in LDS; thread
+    // (g, lane) merges head g's four dims 4*lane..4*lane+3.  A wave that had
+    // no half page left m = -inf, l = acc = 0 and weighs nothing.
+    const float qk_scale = kLog2e / 16.0f;
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+        float lt = st.l[g];  // the four rows hold disjoint tokens
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        mrg_acc[(wave * GP + g) * 64 + lane] = make_float4(st.acc[g][0], st.acc[g][1], st.acc[g][2], st.acc[g][3]);
+        if (lane == 0) {
+            mrg_ml[(wave * GP + g) * 2] = st.m[g];
+            mrg_ml[(wave * GP + g) * 2 + 1] = lt;
+        }
+    }
+    __syncthreads();
+    if (ctx > 0 && qi < GP * 64) {
+        const int g = qi >> 6;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < kWholeWaves; ++v) mm = fmaxf(mm, mrg_ml[(v * GP + g) * 2]);
+        float l = 0.0f;
+        float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int v = 0; v < kWholeWaves; ++v) {
+            const float c = __builtin_amdgcn_exp2f((mrg_ml[(v * GP + g) * 2] - mm) * qk_scale);
+            const float4 x = mrg_acc[(v * GP + g) * 64 + lane];
+            l += mrg_ml[(v * GP + g) * 2 + 1] * c;
+            o.x += x.x * c;
+            o.y += x.y * c;
+            o.z += x.z * c;
+            o.w += x.w * c;
+        }
+        const float inv = 1.0f / l;
+        *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(b) * nh + hq0 + g) * kHeadDim + 4 * lane) =
+            out_fp16x4(o.x * inv, o.y * inv, o.z * inv, o.w * inv, gate_of(a, b, hq0 + g, lane));
+    }
+}
+
+template <int GP>
+hipError_t launch_whole(const DecodeArgs &a, hipStream_t s) {
+    const int units8 = (a.n_seqs * a.num_kv_heads + 7) / 8;
+    hipLaunchKernelGGL(whole_kernel<GP>, dim3(units8 * 8 * a.whole), dim3(64 * kWholeWaves), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int G>
 hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
     // Kv heads per workgroup (two waves each): all of them up to
@@ -656,6 +820,19 @@ hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
 
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s) {
     if (a.n_seqs <= 0) return hipSuccess;
+    if (a.whole) {
+        const int G = a.num_heads / a.num_kv_heads;
+        if (a.whole < 1 || G % a.whole) return hipErrorInvalidValue;
+        switch (G / a.whole) {
+            case 1: return launch_whole<1>(a, s);
+            case 2: return launch_whole<2>(a, s);
+            case 3: return launch_whole<3>(a, s);
+            case 4: return launch_whole<4>(a, s);
+            case 6: return launch_whole<6>(a, s);
+            case 8: return launch_whole<8>(a, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (a.num_heads / a.num_kv_heads) {
         case 1: return launch_g<1>(a, s);
         case 2: return launch_g<2>(a, s);

@@ -54,6 +54,10 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 constexpr int kStageSlots = 4;
 constexpr int kDecodeWgPerCu = 1;   // stream-K decode workgroups per CU
 constexpr int kMinPagesPerWg = 1;   // a short sequence still spreads over several CUs
+// A decode step (automatic split) whose longest sequence has at most this
+// many rows runs the whole-sequence form: one workgroup per sequence and kv
+// head, no partials and no combine launch.
+constexpr int kWholeMaxTokens = 512;
 
 }  // namespace
 
@@ -134,6 +138,7 @@ struct kva_cache {
 
     int32_t split_user = 0;  // decode tokens per workgroup (0 = automatic)
     int32_t last_split = 0, last_nwg = 0;
+    bool last_whole = false;  // the last decode ran the whole-sequence form
 
     // Graph recording (kva_graph_capture_begin .. _end) on `cap_stream`.
     bool capturing = false;
@@ -1017,13 +1022,17 @@ int kva_set_decode_split(kva_cache *c, int32_t split_tokens) {
     return KVA_OK;
 }
 
-// Timeline records: every decode workgroup the workspace can serve, times the
-// grid rows of a cache's own heads, eight waves each.
+// Timeline records, eight waves each: every stream-K workgroup the workspace
+// can serve times the grid rows of a cache's own heads, or one whole-form
+// workgroup per sequence and query head (the most it launches), whichever is
+// more.
 static size_t timeline_words(const kva_cache *c) {
     const int32_t hpw = std::min(c->cfg.num_kv_heads, static_cast<int32_t>(kva::kDecodeHeadsPerWg));
     int32_t h = hpw;
     while (c->cfg.num_kv_heads % h) --h;
-    return static_cast<size_t>(c->max_wg) * (c->cfg.num_kv_heads / h) * 8 * kva::kTimelineWords;
+    const size_t wgs = std::max(static_cast<size_t>(c->max_wg) * (c->cfg.num_kv_heads / h),
+                                static_cast<size_t>(c->cfg.max_seqs) * c->cfg.num_heads);
+    return wgs * 8 * kva::kTimelineWords;
 }
 
 int kva_timeline_enable(kva_cache *c, int32_t on) {
@@ -1048,7 +1057,7 @@ int kva_timeline_read(const kva_cache *c, uint64_t *dst, size_t cap_words, int32
     int32_t h = std::min(c->cfg.num_kv_heads, static_cast<int32_t>(kva::kDecodeHeadsPerWg));
     while (c->cfg.num_kv_heads % h) --h;
     *n_wg = c->last_nwg;
-    *grid_rows = c->cfg.num_kv_heads / h;
+    *grid_rows = c->last_whole ? 1 : c->cfg.num_kv_heads / h;
     const size_t words = static_cast<size_t>(c->last_nwg) * *grid_rows * 8 * kva::kTimelineWords;
     if (cap_words < words) return fail(KVA_ERR_CAPACITY, "timeline needs %zu words, %zu given", words, cap_words);
     KVA_HIP(hipDeviceSynchronize());
@@ -1074,6 +1083,31 @@ static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_
     a.timeline = c->d_timeline;
     c->last_nwg = a.n_wg;
     c->last_split = static_cast<int32_t>((pages * kva::kBlockTokens + a.n_wg - 1) / a.n_wg);
+}
+
+// Switch a decode launch to the whole-sequence form when the split is
+// automatic and no sequence is longer than kWholeMaxTokens rows: returns the
+// workgroups per (sequence, kv head), each serving group / n of its query
+// heads, n as large as fits one workgroup per CU (0: stream-K instead).
+static int32_t use_whole(kva_cache *c, int32_t split_user, int64_t max_ctx, int32_t n_seqs, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t n_cu) {
+    const bool whole = split_user == 0 && max_ctx <= kWholeMaxTokens;
+    if (c) c->last_whole = whole;
+    if (!whole) return 0;
+    const int32_t g = num_heads / num_kv_heads;
+    const int64_t units = static_cast<int64_t>(n_seqs) * num_kv_heads;
+    int32_t n = 1;
+    for (int32_t d = g; d > 1; --d) {  // the most groups whose workgroups fit the CUs
+        if (g % d == 0 && units * d <= n_cu) {
+            n = d;
+            break;
+        }
+    }
+    if (c) {
+        c->last_nwg = static_cast<int32_t>(units * n);
+        c->last_split = 0;
+    }
+    return n;
 }
 
 // The output gate's layout: 8-byte aligned rows, a stride in whole 4-element
@@ -1112,7 +1146,11 @@ static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *g
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
     set_stream_k(c, a, c->st_total_pages, c->cfg.num_heads);
-    if (c->capturing) {
+    if ((a.whole = use_whole(c, c->split_user, c->st_max_ctx, c->st_n_seqs, c->cfg.num_heads,
+                             c->cfg.num_kv_heads, c->n_cu))) {
+        // Every launch of this form reads the lengths from the step plan: a
+        // recorded one stays correct when they grow.
+    } else if (c->capturing) {
         // Recorded launch: the device derives the page count and workgroup
         // count from the step plan at replay; the grid is the cap.
         const int64_t fit = static_cast<int64_t>(c->ws_rows / (2 * static_cast<size_t>(c->cfg.num_heads)));
@@ -1500,10 +1538,20 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
     // Every sequence has the same length: the page prefix sums are implicit.
     const int64_t unit_pages = (kv_seq_len + kva::kBlockTokens - 1) / kva::kBlockTokens;
     const int64_t pages = unit_pages * batch;
-    if (noalloc) {
-        if (num_heads > kva::kNoAllocMaxHeads)
-            return fail(KVA_ERR_CAPACITY, "num_heads %d: the static decode scratch (%zu bytes) serves at most %d heads",
-                        num_heads, kva::kNoAllocScratchBytes, kva::kNoAllocMaxHeads);
+    // Without a workspace (and not the allocation-free entry point) every
+    // length runs the whole-sequence form, which needs none.
+    if (noalloc && num_heads > kva::kNoAllocMaxHeads)
+        return fail(KVA_ERR_CAPACITY, "num_heads %d: the static decode scratch (%zu bytes) serves at most %d heads",
+                    num_heads, kva::kNoAllocScratchBytes, kva::kNoAllocMaxHeads);
+    int n_cu = ws ? ws->n_cu : 0;
+    if (!ws) {
+        int dev = 0;
+        KVA_HIP(hipGetDevice(&dev));
+        KVA_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    }
+    if ((a.whole = use_whole(ws, ws ? ws->split_user : 0, (ws || noalloc) ? kv_seq_len : 0, batch, num_heads,
+                             num_kv_heads, std::max(1, n_cu)))) {
+    } else if (noalloc) {
         void *scratch = nullptr;
         int n_cu = 0;
         KVA_HIP(kva::noalloc_scratch(&scratch, &n_cu));
@@ -1516,14 +1564,8 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
                                   (pages + kMinPagesPerWg - 1) / kMinPagesPerWg, fit})));
         a.ws_acc = static_cast<float *>(scratch);
         a.ws_ml = a.ws_acc + static_cast<size_t>(2) * a.n_wg * num_heads * kva::kHeadDim;
-    } else if (ws) {
-        set_stream_k(ws, a, pages, num_heads);
     } else {
-        // No workspace: one workgroup per sequence, written whole (one CU
-        // per sequence: for short caches; the Python launchers always pass
-        // a workspace).
-        a.total_pages = static_cast<int32_t>(pages);
-        a.n_wg = batch;
+        set_stream_k(ws, a, pages, num_heads);
     }
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));

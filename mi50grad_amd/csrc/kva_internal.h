@@ -147,8 +147,13 @@ struct DecodeArgs {
     // Per-workgroup timeline (null = off): record kTimelineWords words per
     // wave, [n_wg][grid rows][8 waves], see kva_timeline_read.
     uint64_t *timeline;
+    // > 0: whole-sequence form, one workgroup per (sequence, kv head, group
+    // of G / whole query heads): no partials, no combine; the stream-K
+    // fields are unused.  G / whole must be 1, 2, 3, 4, 6 or 8.
+    int32_t whole;
 };
 constexpr int kTimelineWords = 4;
+constexpr int kWholeWaves = 8;  // waves per whole-sequence decode workgroup
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
 
 // Static device scratch of kva_legacy_decode_noalloc (k_noalloc.hip): the

@@ -92,6 +92,34 @@ def test_decode_ragged_permuted(device, split):
     cache.destroy()
 
 
+@pytest.mark.parametrize("split", [0, 16])
+def test_decode_short_steps(device, split):
+    """A step whose longest sequence is at most 512 rows: the automatic split
+    runs the whole-sequence form (one workgroup per sequence and kv head, its
+    eight waves merged in LDS, no combine), a forced split stream-K; both
+    within 2e-3 of the oracle at every page-edge length up to the limit."""
+    rng = np.random.default_rng(500 + split)
+    lengths = [0, 1, 6, 7, 8, 9, 15, 16, 17, 31, 63, 64, 65, 127, 128, 200, 255, 256, 300, 383, 510, 511]
+    nblk = [(L + 1 + 15) // 16 for L in lengths]
+    perm = rng.permutation(sum(nblk))
+    ids, o = [], 0
+    for n in nblk:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say(f"decode short steps split={split}")
+    cache, kr, vr = build_cache(lengths, ids, extra_rows=1, rng=rng)
+    tables = Tables(device, 1024)
+    got, exp, *_ = run_decode_step(device, cache, kr, vr, lengths, rng, tables, split=split)
+    assert max_err(got, exp) <= TOL, cache.decode_split()
+    used, n_wg = cache.decode_split()
+    if split == 0:  # workgroups: each (sequence, kv head) split into groups of its query heads
+        units = len(lengths) * HKV
+        assert used == 0 and n_wg % units == 0 and (H // HKV) % (n_wg // units) == 0, (used, n_wg)
+    else:
+        assert used == split
+    cache.destroy()
+
+
 @pytest.mark.parametrize("split", [0, 64, 128, 256])
 def test_decode_many_short_sequences(device, split):
     """Workgroup page ranges that start, end and span many (sequence, kv head)

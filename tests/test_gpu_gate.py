@@ -33,17 +33,19 @@ def ulps(a, b):
     return np.abs(_ordered(a) - _ordered(b))
 
 
-@pytest.mark.parametrize("split", [0, 64])
-def test_decode_gated_paged(device, split):
-    rng = np.random.default_rng(21 + split)
-    lengths = [1, 15, 16, 300, 2047]
+@pytest.mark.parametrize("split,lengths", [(0, [1, 15, 16, 300, 2047]), (64, [1, 15, 16, 300, 2047]),
+                                           (0, [1, 15, 16, 300, 511])])
+def test_decode_gated_paged(device, split, lengths):
+    """Stream-K (the first two cases) and the whole-sequence form (the last:
+    every sequence at most 512 rows at the automatic split)."""
+    rng = np.random.default_rng(21 + split + (0 if lengths[-1] == 2047 else 1000))
     nblk = [(L + 1 + 15) // 16 for L in lengths]
     perm = rng.permutation(sum(nblk))
     ids, o = [], 0
     for n in nblk:
         ids.append([int(x) for x in perm[o:o + n]])
         o += n
-    say(f"decode gated split={split}")
+    say(f"decode gated split={split} longest={lengths[-1]}")
     cache, kr, vr = build_cache(lengths, ids, extra_rows=1, rng=rng)
     cache.set_decode_split(split)
     tables = Tables(device, 4096)

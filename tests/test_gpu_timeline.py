@@ -2,9 +2,10 @@
 
 The records must describe the launch that ran (one per wave of every
 workgroup, entry <= first K/V issue <= walk end, an XCD id below 8, page
-counts that add up to the step's pages) and recording must not change the
-decode's output (bit-equal to the same decode with the timeline off).
-Refused before it is enabled.
+counts that add up to the step's pages; for the whole-sequence form, one
+workgroup per sequence and kv head with that sequence's pages) and recording
+must not change the decode's output (bit-equal to the same decode with the
+timeline off).  Refused before it is enabled.
 """
 import numpy as np
 import pytest
@@ -50,4 +51,42 @@ def test_timeline_records_the_launch_and_leaves_the_output_alone():
     cache.timeline_enable(False)
     with pytest.raises(_lib.KvaError, match="not enabled"):
         cache.timeline()
+    cache.destroy()
+
+
+def test_timeline_of_the_whole_sequence_form():
+    """A step of short sequences runs the whole-sequence form: one record per
+    wave of each of its workgroups (sequence-major, several per sequence),
+    carrying that sequence's page count; the output is again unchanged by
+    recording."""
+    dev = GPUDevice(0)
+    rng = np.random.default_rng(12)
+    lengths = [40, 0, 300, 17]
+    npg = [(n + 1 + 15) // 16 for n in lengths]
+    perm = rng.permutation(sum(npg))
+    ids, o = [], 0
+    for n in npg:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say("timeline: whole-sequence form, 4 short sequences")
+    cache, _, _ = build_cache(lengths, ids, extra_rows=1, rng=rng)
+    cache.begin_step([0, 1, 2, 3], [1, 1, 1, 1])
+    q = dev.array(rng.standard_normal((4, H, D), dtype=np.float32).astype(np.float16))
+    out_off, out_on = dev.empty((4, H, D), np.float16), dev.empty((4, H, D), np.float16)
+    cache.decode(0, q, out_off)
+    cache.timeline_enable(True)
+    cache.decode(0, q, out_on)
+    rec = cache.timeline()
+    split, n_wg = cache.decode_split()
+    per_seq = n_wg // 4  # workgroups per sequence: kv heads x query-head groups
+    assert split == 0 and n_wg % (4 * HKV) == 0
+    assert rec.shape == (n_wg, 1, 8, 4)
+    assert np.array_equal(out_on.numpy().view(np.uint16), out_off.numpy().view(np.uint16))
+    ent, first, end, meta = (rec[..., i] for i in range(4))
+    assert (ent > 0).all() and (ent <= first).all() and (first <= end).all()
+    assert (((meta >> 32) & 0xF) < 8).all()
+    pages = (meta & 0xFFFFFFFF)[:, 0, 0]
+    assert [int(x) for x in pages] == [n for n in npg for _ in range(per_seq)]
+    assert (meta[:, :, :1] == meta).all()  # every wave of a workgroup reports the same
+    cache.timeline_enable(False)
     cache.destroy()
