@@ -262,7 +262,7 @@ int kva_rollback(kva_cache *cache, int32_t n_seqs, const int32_t *seq_ids,
                  const int32_t *keep_rows, kva_stream_t stream);
 
 /* Split-K tuning for kva_decode: tokens per split (multiple of 16); 0 =
- * automatic.  Automatic runs a step whose longest sequence is at most 512
+ * automatic.  Automatic runs a step whose longest sequence is at most 1024
  * rows in the whole-sequence form (each sequence walked whole by workgroups
  * that split its kv heads' query-head groups among them, no partials, no
  * combine launch; kva_get_decode_split then reports split 0 and the

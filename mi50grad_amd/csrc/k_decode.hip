@@ -562,22 +562,28 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
 }
 
 // Merge the partials of one (sequence, kv head, query head of the group)
-// whose pages were cut across workgroups: 64 lanes x 4 dims.  A separate
-// launch (stream order makes the partials visible), so no cross-workgroup
-// fences are needed: an agent-scope release on every decode workgroup costs
-// an L2 writeback per workgroup on multi-XCD parts.  The (m, l) pairs and acc
-// rows of up to kChunk partials are all requested before any is used, so a
-// sequence cut into at most kChunk pieces costs two memory round trips (its
-// length, then its partials).
+// whose pages were cut across workgroups: 64 lanes x 4 dims per wave.  A
+// separate launch (stream order makes the partials visible), so no
+// cross-workgroup fences are needed: an agent-scope release on every decode
+// workgroup costs an L2 writeback per workgroup on multi-XCD parts.  The
+// (m, l) pairs and acc rows of up to kChunk partials are all requested before
+// any is used, so a sequence cut into at most kChunk pieces costs two memory
+// round trips (its length, then its partials), taken by wave 0 alone.  A
+// sequence cut into more pieces (one long sequence over every CU) has its
+// chunks dealt to the kCombineWaves waves, which merge through LDS.
+constexpr int kCombineWaves = 4;
 template <int G>
-__global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs a) {
     constexpr int kChunk = 16;
+    __shared__ float4 w_acc[kCombineWaves * 64];
+    __shared__ float w_ml[kCombineWaves * 2];
     const int u = blockIdx.x;
     const int g = blockIdx.y;
     const int hkv = a.num_kv_heads;
     const int b = u / hkv;
     const int h = u - b * hkv;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int P, W;
     stream_k_shape(a, P, W);
     const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
@@ -588,6 +594,8 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
     const int w1 = wg_of_page(first + npg - 1, P, W);
     if (w0 == w1) return;  // one workgroup covered the sequence and wrote it
     const int n = w1 - w0 + 1;
+    const bool multi = n > kChunk;  // uniform over the workgroup
+    if (!multi && wave != 0) return;
     // Partial i comes from workgroup w0 + i: slot 2w when the sequence began
     // at or before that workgroup's range, else 2w+1.
     auto row_of = [&](int i) -> size_t {
@@ -595,10 +603,12 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
         const int slot = 2 * w + (first <= wg_start(w, P, W) ? 0 : 1);
         return (static_cast<size_t>(slot) * hkv + h) * G + g;
     };
-    // Running merge over chunks: (big, lt, at) is the merge of the chunks so far.
+    // Running merge over this wave's chunks: (big, lt, at) is the merge of
+    // the chunks so far (big = -inf, lt = 0 before any).
     float big = -INFINITY, lt = 0.0f;
     float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c0 = 0; c0 < n; c0 += kChunk) {
+    const int step = multi ? kCombineWaves * kChunk : kChunk;
+    for (int c0 = (multi ? wave : 0) * kChunk; c0 < n; c0 += step) {
         const int cnt = min(kChunk, n - c0);
         float2 ml = make_float2(-INFINITY, 0.0f);
         if (lane < cnt) ml = *reinterpret_cast<const float2 *>(a.ws_ml + row_of(c0 + lane) * 2);
@@ -631,6 +641,32 @@ __global__ __launch_bounds__(64) void combine_kernel(DecodeArgs a) {
             at.w += ck * v[k].w;
         }
         big = nb;
+    }
+    if (multi) {
+        // Wave 0 always holds a chunk; a wave without one (fewer than
+        // kCombineWaves chunks) keeps big = -inf and weighs 0.
+        w_acc[wave * 64 + lane] = at;
+        if (lane == 0) {
+            w_ml[wave * 2] = big;
+            w_ml[wave * 2 + 1] = lt;
+        }
+        __syncthreads();
+        if (wave != 0) return;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < kCombineWaves; ++v) mm = fmaxf(mm, w_ml[v * 2]);
+        lt = 0.0f;
+        at = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int v = 0; v < kCombineWaves; ++v) {
+            const float c = __builtin_amdgcn_exp2f(w_ml[v * 2] - mm);  // 0 for a wave without chunks
+            const float4 x = w_acc[v * 64 + lane];
+            lt += w_ml[v * 2 + 1] * c;
+            at.x += x.x * c;
+            at.y += x.y * c;
+            at.z += x.z * c;
+            at.w += x.w * c;
+        }
     }
     const float inv = 1.0f / lt;
     *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(b) * a.num_heads + h * G + g) * kHeadDim +
@@ -812,7 +848,7 @@ hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(decode_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(128 * hpw), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !a.ws_acc) return e;
-    hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * kCombineWaves), 0, s, a);
     return hipGetLastError();
 }
 

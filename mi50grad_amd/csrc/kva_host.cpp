@@ -57,7 +57,7 @@ constexpr int kMinPagesPerWg = 1;   // a short sequence still spreads over sever
 // A decode step (automatic split) whose longest sequence has at most this
 // many rows runs the whole-sequence form: one workgroup per sequence and kv
 // head, no partials and no combine launch.
-constexpr int kWholeMaxTokens = 512;
+constexpr int kWholeMaxTokens = 1024;
 
 }  // namespace
 

@@ -94,12 +94,14 @@ def test_decode_ragged_permuted(device, split):
 
 @pytest.mark.parametrize("split", [0, 16])
 def test_decode_short_steps(device, split):
-    """A step whose longest sequence is at most 512 rows: the automatic split
-    runs the whole-sequence form (one workgroup per sequence and kv head, its
-    eight waves merged in LDS, no combine), a forced split stream-K; both
-    within 2e-3 of the oracle at every page-edge length up to the limit."""
+    """A step whose longest sequence is at most 1024 rows: the automatic split
+    runs the whole-sequence form (workgroups per sequence, kv head and group
+    of query heads, eight waves merged in LDS, no combine), a forced split
+    stream-K; both within 2e-3 of the oracle at page-edge lengths up to the
+    limit."""
     rng = np.random.default_rng(500 + split)
-    lengths = [0, 1, 6, 7, 8, 9, 15, 16, 17, 31, 63, 64, 65, 127, 128, 200, 255, 256, 300, 383, 510, 511]
+    lengths = [0, 1, 6, 7, 8, 9, 15, 16, 17, 31, 63, 64, 65, 127, 128, 200, 255, 256, 300, 383, 510, 511,
+               700, 1000, 1023]
     nblk = [(L + 1 + 15) // 16 for L in lengths]
     perm = rng.permutation(sum(nblk))
     ids, o = [], 0

@@ -37,7 +37,7 @@ def ulps(a, b):
                                            (0, [1, 15, 16, 300, 511])])
 def test_decode_gated_paged(device, split, lengths):
     """Stream-K (the first two cases) and the whole-sequence form (the last:
-    every sequence at most 512 rows at the automatic split)."""
+    every sequence at most 1024 rows at the automatic split)."""
     rng = np.random.default_rng(21 + split + (0 if lengths[-1] == 2047 else 1000))
     nblk = [(L + 1 + 15) // 16 for L in lengths]
     perm = rng.permutation(sum(nblk))
