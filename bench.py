@@ -373,9 +373,10 @@ def _cpu_model() -> str:
 def c1_workload(dev, reps=200):
     """Config 1: one layer, batch 1, 255 cached rows; append at position 255
     (norm + RoPE of q and k, K/V into the cache) then decode over 256 rows.
-    GPU: HIP events around append + decode, median of `reps` calls, L2 and
-    MALL flushed before each call (the layer's 1 MB would otherwise stay
-    cached from the previous call).  CPU: the
+    GPU: HIP events around kva_append_decode (one launch), and separately
+    around kva_append_qknorm_rope + kva_decode, median of `reps` calls each,
+    L2 and MALL flushed before each call (the layer's 1 MB would otherwise
+    stay cached from the previous call).  CPU: the
     numpy oracle's same step (norm + RoPE of the 28 rows, then decode
     attention), median of 25 calls with 1 BLAS thread and with all of them."""
     from threadpoolctl import threadpool_limits
@@ -401,22 +402,27 @@ def c1_workload(dev, reps=200):
     q, k, v = dev.empty((1, H, D), np.float16), dev.array(x.k_new), dev.array(x.v_new)
     out = dev.empty((1, H, D), np.float16)
     flush = L2Flush(dev)
-    ms = []
-    for i in range(reps + 10):
-        cache.set_len(0, 255)
-        cache.begin_step([0], [1])
-        dev.upload(q.ptr, x.q.tobytes())
-        flush()
-        a, b = Event(), Event()
-        a.record()
-        cache.append(0, q, k, v, qw, kw, d_cos, d_sin, 256)
-        cache.decode(0, q, out)
-        b.record()
-        b.synchronize()
-        if i >= 10:
-            ms.append(a.elapsed_ms(b))
-        a.destroy()
-        b.destroy()
+    ms = {"fused": [], "two_calls": []}
+    for mode, times in ms.items():
+        for i in range(reps + 10):
+            cache.set_len(0, 255)
+            cache.begin_step([0], [1])
+            dev.upload(q.ptr, x.q.tobytes())
+            dev.upload(k.ptr, x.k_new.tobytes())
+            flush()
+            a, b = Event(), Event()
+            a.record()
+            if mode == "fused":
+                cache.append_decode(0, q, k, v, qw, kw, d_cos, d_sin, 256, out)
+            else:
+                cache.append(0, q, k, v, qw, kw, d_cos, d_sin, 256)
+                cache.decode(0, q, out)
+            b.record()
+            b.synchronize()
+            if i >= 10:
+                times.append(a.elapsed_ms(b))
+            a.destroy()
+            b.destroy()
     cache.destroy()
     flush.free()
 
@@ -439,14 +445,17 @@ def c1_workload(dev, reps=200):
                 cpu_step()
                 ts.append(time.perf_counter() - t0)
         cpu[label] = float(np.median(ts) * 1e6)
-    return {"gpu_us": float(np.median(ms) * 1e3), "gpu_min_us": float(np.min(ms) * 1e3), "cpu_us_1": cpu["1"],
+    return {"gpu_us": float(np.median(ms["fused"]) * 1e3), "gpu_min_us": float(np.min(ms["fused"]) * 1e3),
+            "two_calls_us": float(np.median(ms["two_calls"]) * 1e3), "cpu_us_1": cpu["1"],
             "cpu_us_all": cpu["all"], "reps": reps}
 
 
-def c2_workload(dev, steps_unused, warmup, graph=False, split=0):
-    """Config 2: B=1, 16 layers, 128 decode steps from a 128-row cache.  With
-    graph=True the 16 layers' append + decode are recorded once (kva_graph_*)
-    and replayed after each step's plan upload.
+def c2_workload(dev, steps_unused, warmup, graph=False, split=0, fused=True):
+    """Config 2: B=1, 16 layers, 128 decode steps from a 128-row cache.  Each
+    layer is one kva_append_decode call (fused=True: norm + RoPE, append and
+    decode in one launch) or kva_append_qknorm_rope + kva_decode.  With
+    graph=True the 16 layers' calls are recorded once (kva_graph_*) and
+    replayed after each step's plan upload.
 
     Timed twice: back to back (wall clock over the 128 steps, the 16 MB of
     pages staying in the MALL), and per step between HIP events on the launch
@@ -468,8 +477,11 @@ def c2_workload(dev, steps_unused, warmup, graph=False, split=0):
 
     def layers():
         for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
-            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 256, stream=sh)
-            cache.decode(layer, q, out, stream=sh)
+            if fused:
+                cache.append_decode(layer, q, k, v, qw, kw, d_cos, d_sin, 256, out, stream=sh)
+            else:
+                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 256, stream=sh)
+                cache.decode(layer, q, out, stream=sh)
 
     def run(evs=None, flush=None):
         cache.set_len(0, start)
@@ -818,8 +830,9 @@ def main() -> int:
             "metric": "config-1 one-layer step latency (append at 255 + decode over 256, B=1)",
             "value": r["gpu_us"], "unit": "us", "n_gpus": 1, "steps": r["reps"], "higher_is_better": False,
             "dtype": "f16", "data": "synthetic (seed 0, the config-1 recipe)",
-            "config": {"workload": "C1", "layers": 1, "rows": 256},
+            "config": {"workload": "C1", "layers": 1, "rows": 256, "calls": "kva_append_decode"},
             "gpu_min_us": r["gpu_min_us"], "alg_bytes": by, "gpu_gbs": by / (r["gpu_us"] * 1e-6) / 1e9,
+            "two_calls_us": r["two_calls_us"],
             "cpu_baseline": {"value": r["cpu_us_1"], "unit": "us", "cores": 1, "kind": "port",
                              "all_threads_us": r["cpu_us_all"], "host_logical_cpus": os.cpu_count(),
                              "cpu_model": _cpu_model(),
@@ -829,6 +842,7 @@ def main() -> int:
     if args.workload in ("c2", "c2graph"):
         graph = args.workload == "c2graph"
         r = c2_workload(dev, args.steps, args.warmup, graph=graph, split=args.split)
+        r2 = c2_workload(dev, args.steps, args.warmup, graph=graph, split=args.split, fused=False)
         ms = r["step_us"] * 1e-3
         warm_us = r["wall_s"] * 1e6 / r["steps"]
         print(json.dumps({"metric": "config-2 decode step time (16 layers, B=1, 128->256 rows)",
@@ -840,8 +854,11 @@ def main() -> int:
                           "kv_gbs": r["kv_bytes"] / r["steps"] / (r["step_us"] * 1e-6) / 1e9,
                           "back_to_back_us_per_step": warm_us, "dtype": "f16",
                           "data": "synthetic",
-                          "config": {"workload": "C2", "dispatch": "recorded step replay" if graph
-                                     else "per-layer calls"}}))
+                          "two_calls_per_layer": {"step_us": r2["step_us"],
+                                                  "back_to_back_us_per_step": r2["wall_s"] * 1e6 / r2["steps"],
+                                                  "calls": "kva_append_qknorm_rope + kva_decode"},
+                          "config": {"workload": "C2", "calls": "kva_append_decode per layer",
+                                     "dispatch": "recorded step replay" if graph else "per-layer calls"}}))
         return 0
 
     if args.workload == "proj":

@@ -224,6 +224,25 @@ int kva_decode(kva_cache *cache, int32_t layer, const void *q, void *out,
  * [Q | Q_gate] projection output, engine.py:1069-1071); 8-byte aligned.     */
 int kva_decode_gated(kva_cache *cache, int32_t layer, const void *q, const void *gate,
                      int64_t gate_stride, void *out, kva_stream_t stream);
+/* kva_append_qknorm_rope followed by kva_decode for a step of one new token
+ * per sequence, in one launch when the decode runs the whole-sequence form
+ * (see kva_set_decode_split) and in two otherwise.  Replaces the decode
+ * loop's qknorm_q, qknorm_k (cache write), K/V copy and decode_attn launches
+ * (c_dispatch.c:1066-1103).  The same results as the two calls: q is
+ * normalised and rotated in place and the cache rows are bit-identical;
+ * out is the decode over every row including the new one (the new token's
+ * score and V row enter from registers, so its rounding path differs from
+ * kva_decode's: both are within the decode's tolerance).  Unlike
+ * kva_append_qknorm_rope, k is only read.                                   */
+int kva_append_decode(kva_cache *cache, int32_t layer, void *q, const void *k, const void *v,
+                      const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                      const void *sin_tab, int32_t table_rows, void *out, kva_stream_t stream);
+/* kva_append_decode with the output gate of kva_decode_gated (the decode
+ * loop's sigmoid_mul launch, c_dispatch.c:1105).                           */
+int kva_append_decode_gated(kva_cache *cache, int32_t layer, void *q, const void *k, const void *v,
+                            const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                            const void *sin_tab, int32_t table_rows, const void *gate,
+                            int64_t gate_stride, void *out, kva_stream_t stream);
 /* Causal attention of each sequence's new rows over cache + new rows: new
  * token i (slot s) sees slots [0, s].  Replaces the prefill attention of
  * _prefill_full_attention (engine.py:3043-3139; flash_attn_256_fp16,

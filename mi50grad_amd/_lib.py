@@ -71,6 +71,8 @@ SIGNATURES = {
     "kva_out_project": [_P, _P, _I, _I, _P, _I, _P, _P, _P],
     "kva_decode": [_P, _I, _P, _P, _P],
     "kva_decode_gated": [_P, _I, _P, _P, c_int64, _P, _P],
+    "kva_append_decode": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P],
+    "kva_append_decode_gated": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, c_int64, _P, _P],
     "kva_prefill": [_P, _I, _P, _P, _P],
     "kva_tree_verify": [_P, _I, _P, _P, _P],
     "kva_prefill_gated": [_P, _I, _P, _P, c_int64, _P, _P],

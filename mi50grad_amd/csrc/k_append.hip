@@ -46,7 +46,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         const uint4 xin = ld16(x + 8 * lane);
         const NormRopeIn nin = norm_rope_in<32>(a.k_w, cos_row, sin_row, a.half_rot, lane);
         const uint4 y = norm_rope_apply<32>(xin, nin, a.half_rot, a.eps, lane);
-        st16(x + 8 * lane, y);
+        if (!a.keep_k) st16(x + 8 * lane, y);
         st16(a.k_pool + (row_base + kh) * kHeadDim + 8 * lane, y);
     } else {
         const int vh = hr - a.num_heads - hkv;

@@ -29,6 +29,7 @@
 //       are paired so one v_dot2_f32_f16 folds two tokens; the pair's
 //       probabilities (row t's) reach every lane by an LDS broadcast.
 #include "k_common.h"
+#include "k_normrope.h"
 #include "kva_internal.h"
 
 namespace kva {
@@ -687,12 +688,20 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs 
 // XCD and their reads of its K/V after the first come from that XCD's L2.
 // Correct for any length (a recorded launch keeps this form when the lengths
 // grow), fast while every sequence is a few hundred rows.
-template <int GP>
+//
+// kFused: the step's append runs in the same launch (DecodeArgs::fused).
+// Half-wave k of the workgroup normalises and rotates query row k (k < GP),
+// the kv head's new K row (k = GP) or carries its V row (k = GP + 1), with
+// the append kernel's arithmetic (norm_rope_apply: the same bits); the walk
+// covers the ctx - 1 cached rows and the new token enters the merge as one
+// more partial (its score from the rounded K row, probability 1, its V row).
+template <int GP, bool kFused>
 __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     __shared__ uint4 q_lds[GP * 32];
+    __shared__ uint4 kv_new[kFused ? 64 : 1];  // fused: the new K (normalised) and V rows
     __shared__ uint32_t p_lds[kWholeWaves * 32];
     __shared__ float4 mrg_acc[kWholeWaves * GP * 64];
-    __shared__ float mrg_ml[kWholeWaves * GP * 2];
+    __shared__ float mrg_ml[(kWholeWaves + 1) * GP * 2];
     __shared__ uint64_t tl_t[2];  // timeline: entry and first-issue times
     if (a.timeline && threadIdx.x == 0) tl_t[0] = __builtin_amdgcn_s_memrealtime();
     const int hkv = a.num_kv_heads;
@@ -711,6 +720,8 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     // output.
     const int ctx = a.ctx_lens ? ld_uniform(a.ctx_lens + b) : a.ctx_len_const;
     const int sid = a.table ? ld_uniform(a.seq_ids + b) : 0;
+    const int pos = kFused ? ld_uniform(a.app.tok_pos + b) : 0;
+    const int walk = kFused ? ctx - 1 : ctx;  // cached rows the waves walk
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r = lane >> 4;
@@ -724,12 +735,26 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     const int32_t *row = a.table ? a.table + static_cast<size_t>(sid) * a.table_stride : nullptr;
     const int npg = (max(ctx, 0) + kBlockTokens - 1) / kBlockTokens;
     const int ids = (row && lane < npg) ? row[lane] : 0;
-    // The GP query rows, requested before the first K/V loads.
+    // The GP query rows (fused: and the new K, V rows with the norm weights
+    // and this position's cos/sin), requested before the first K/V loads.
     const int qi = threadIdx.x;
+    const int hw = threadIdx.x >> 5;  // fused: the half-wave's row
+    const int l32 = threadIdx.x & 31;
     uint4 qin = make_uint4(0, 0, 0, 0);
-    if (qi < GP * 32) qin = ld16(a.q + (static_cast<size_t>(b) * nh + hq0) * kHeadDim + 8 * qi);
+    NormRopeIn nin{};
+    if constexpr (kFused) {
+        const AppendArgs &ap = a.app;
+        const uint16_t *src = hw < GP    ? ap.q + (static_cast<size_t>(b) * nh + hq0 + hw) * kHeadDim
+                              : hw == GP ? ap.k + (static_cast<size_t>(b) * hkv + h) * kHeadDim
+                                         : ap.v + (static_cast<size_t>(b) * hkv + h) * kHeadDim;
+        if (hw <= GP + 1) qin = ld16(src + 8 * l32);
+        nin = norm_rope_in<32>(hw < GP ? ap.q_w : ap.k_w, ap.cos_tab + static_cast<size_t>(pos) * ap.half_rot,
+                               ap.sin_tab + static_cast<size_t>(pos) * ap.half_rot, ap.half_rot, l32);
+    } else {
+        if (qi < GP * 32) qin = ld16(a.q + (static_cast<size_t>(b) * nh + hq0) * kHeadDim + 8 * qi);
+    }
 
-    const int n_hp = (max(ctx, 0) + kHalf - 1) / kHalf;
+    const int n_hp = (max(walk, 0) + kHalf - 1) / kHalf;
     const int n_i = wave < n_hp ? (n_hp - wave + kWholeWaves - 1) / kWholeWaves : 0;
     const uint32_t koff = r * row_bytes + 16 * j;
     const uint32_t voff = 8 * lane;
@@ -741,14 +766,38 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
         int id = pg;
         if (row) id = pg < 64 ? __builtin_amdgcn_readlane(ids, pg) : ld_uniform(row + pg);
         const size_t ofs = static_cast<size_t>(id) * page_bytes + static_cast<size_t>(hp & 1) * kHalf * row_bytes;
-        load_half(p, kpool + ofs, vpool + ofs, min(kHalf, ctx - hp * kHalf), on, koff, voff, row_bytes);
+        load_half(p, kpool + ofs, vpool + ofs, min(kHalf, walk - hp * kHalf), on, koff, voff, row_bytes);
     };
     constexpr int kStages = GP <= 6 ? 3 : 2;
     HalfPage A, B, C;
     issue(A, 0);
     if (kStages == 3) issue(B, 1);
     if (a.timeline && threadIdx.x == 0) tl_t[1] = __builtin_amdgcn_s_memrealtime();
-    if (qi < GP * 32) q_lds[qi] = qin;
+    if constexpr (kFused) {
+        const AppendArgs &ap = a.app;
+        // Every half-wave runs the arithmetic (the unused ones on zeros) so
+        // the butterfly's lanes are all active; the results are kept by row.
+        const uint4 y = norm_rope_apply<32>(qin, nin, ap.half_rot, ap.eps, l32);
+        if (hw < GP) {
+            q_lds[hw * 32 + l32] = y;
+            st16(ap.q + (static_cast<size_t>(b) * nh + hq0 + hw) * kHeadDim + 8 * l32, y);
+        } else if (hw == GP) {
+            kv_new[l32] = y;
+        } else if (hw == GP + 1) {
+            kv_new[32 + l32] = qin;
+        }
+        // The first head group of (b, h) writes the new rows into slot ctx - 1.
+        const int slot = ctx - 1;
+        const int pg = max(slot, 0) >> 4;
+        int id = pg;
+        if (row) id = pg < 64 ? __builtin_amdgcn_readlane(ids, pg) : ld_uniform(row + pg);
+        if (z == 0 && ctx > 0 && (hw == GP || hw == GP + 1)) {
+            const size_t at = ((static_cast<size_t>(id) * kBlockTokens + (slot & 15)) * hkv + h) * kHeadDim + 8 * l32;
+            st16((hw == GP ? ap.k_pool : ap.v_pool) + at, hw == GP ? y : qin);
+        }
+    } else {
+        if (qi < GP * 32) q_lds[qi] = qin;
+    }
     __syncthreads();
     uint4 qv[GP][2];
 #pragma unroll
@@ -764,7 +813,7 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
         issue(nr, i + kStages - 1);
         __builtin_amdgcn_sched_barrier(0);
         if (i < n_i) {
-            compute_half<GP>(st, cr, qv, r, j, min(kHalf, ctx - (wave + kWholeWaves * i) * kHalf),
+            compute_half<GP>(st, cr, qv, r, j, min(kHalf, walk - (wave + kWholeWaves * i) * kHalf),
                              p_lds + 32 * wave);
         } else {
             consume(cr);
@@ -794,8 +843,24 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
 
     // Merge the eight waves: each leaves (m, l, acc) in LDS; thread
     // (g, lane) merges head g's four dims 4*lane..4*lane+3.  A wave that had
-    // no half page left m = -inf, l = acc = 0 and weighs nothing.
+    // no half page left m = -inf, l = acc = 0 and weighs nothing.  Fused:
+    // wave g < GP adds head g's score of the new token as partial 8 (its V
+    // row is read from LDS at the merge).
     const float qk_scale = kLog2e / 16.0f;
+    if constexpr (kFused) {
+        if (wave < GP) {
+            const uint2 qq = reinterpret_cast<const uint2 *>(q_lds + wave * 32)[lane];
+            const uint2 kk = reinterpret_cast<const uint2 *>(kv_new)[lane];
+            float sc = dot2(qq.y, kk.y, dot2(qq.x, kk.x, 0.0f));
+            sc = row16_sum(sc);
+            sc += __shfl_xor(sc, 16);
+            sc += __shfl_xor(sc, 32);
+            if (lane == 0) {
+                mrg_ml[(kWholeWaves * GP + wave) * 2] = sc;
+                mrg_ml[(kWholeWaves * GP + wave) * 2 + 1] = 1.0f;
+            }
+        }
+    }
 #pragma unroll
     for (int g = 0; g < GP; ++g) {
         float lt = st.l[g];  // the four rows hold disjoint tokens
@@ -811,14 +876,21 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     if (ctx > 0 && qi < GP * 64) {
         const int g = qi >> 6;
         float mm = -INFINITY;
+        constexpr int kParts = kFused ? kWholeWaves + 1 : kWholeWaves;
 #pragma unroll
-        for (int v = 0; v < kWholeWaves; ++v) mm = fmaxf(mm, mrg_ml[(v * GP + g) * 2]);
+        for (int v = 0; v < kParts; ++v) mm = fmaxf(mm, mrg_ml[(v * GP + g) * 2]);
         float l = 0.0f;
         float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int v = 0; v < kWholeWaves; ++v) {
+        for (int v = 0; v < kParts; ++v) {
             const float c = __builtin_amdgcn_exp2f((mrg_ml[(v * GP + g) * 2] - mm) * qk_scale);
-            const float4 x = mrg_acc[(v * GP + g) * 64 + lane];
+            float4 x;
+            if (v < kWholeWaves) {
+                x = mrg_acc[(v * GP + g) * 64 + lane];
+            } else {
+                const uint2 vv = reinterpret_cast<const uint2 *>(kv_new + 32)[lane];
+                x = make_float4(lo_f(vv.x), hi_f(vv.x), lo_f(vv.y), hi_f(vv.y));
+            }
             l += mrg_ml[(v * GP + g) * 2 + 1] * c;
             o.x += x.x * c;
             o.y += x.y * c;
@@ -834,7 +906,11 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
 template <int GP>
 hipError_t launch_whole(const DecodeArgs &a, hipStream_t s) {
     const int units8 = (a.n_seqs * a.num_kv_heads + 7) / 8;
-    hipLaunchKernelGGL(whole_kernel<GP>, dim3(units8 * 8 * a.whole), dim3(64 * kWholeWaves), 0, s, a);
+    const dim3 grid(units8 * 8 * a.whole), block(64 * kWholeWaves);
+    if (a.fused)
+        hipLaunchKernelGGL((whole_kernel<GP, true>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((whole_kernel<GP, false>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 

@@ -785,14 +785,11 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     return KVA_OK;
 }
 
-static int append_impl(kva_cache *c, int32_t layer, void *q, void *k, const void *v, const void *q_norm_w,
+// Check an append's operands (the step already begun) and fill its launch
+// arguments.
+static int make_append(kva_cache *c, int32_t layer, void *q, void *k, const void *v, const void *q_norm_w,
                        const void *k_norm_w, const void *cos_tab, const void *sin_tab, int32_t table_rows,
-                       kva_stream_t stream) {
-    int rc = require_device(c);
-    if (rc) return rc;
-    if ((rc = check_layer(c, layer))) return rc;
-    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
-    if (c->st_n_tok == 0) return KVA_OK;
+                       kva::AppendArgs &a) {
     if (!q || !k || !v || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab)
         return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(q_norm_w) || !aligned16(k_norm_w))
@@ -803,7 +800,7 @@ static int append_impl(kva_cache *c, int32_t layer, void *q, void *k, const void
     if (c->st_max_pos >= table_rows)
         return fail(KVA_ERR_INVALID_ARG, "RoPE position %d beyond the %d table rows", c->st_max_pos,
                     table_rows);
-    kva::AppendArgs a{};
+    a = kva::AppendArgs{};
     a.q = static_cast<uint16_t *>(q);
     a.k = static_cast<uint16_t *>(k);
     a.v = static_cast<const uint16_t *>(v);
@@ -823,6 +820,19 @@ static int append_impl(kva_cache *c, int32_t layer, void *q, void *k, const void
     a.num_kv_heads = c->cfg.num_kv_heads;
     a.half_rot = half_rot;
     a.eps = c->cfg.eps;
+    return KVA_OK;
+}
+
+static int append_impl(kva_cache *c, int32_t layer, void *q, void *k, const void *v, const void *q_norm_w,
+                       const void *k_norm_w, const void *cos_tab, const void *sin_tab, int32_t table_rows,
+                       kva_stream_t stream) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    if (c->st_n_tok == 0) return KVA_OK;
+    kva::AppendArgs a;
+    if ((rc = make_append(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, a))) return rc;
     KVA_HIP(kva::launch_append(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;
 }
@@ -1121,8 +1131,10 @@ static int check_gate(const void *gate, int64_t gate_stride, int32_t num_heads) 
     return KVA_OK;
 }
 
+// app (nullable): the step's append, fused into the launch when the decode
+// runs the whole-sequence form, else launched first (k left unwritten).
 static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *gate, int64_t gate_stride,
-                       void *out, kva_stream_t stream) {
+                       void *out, kva_stream_t stream, const kva::AppendArgs *app = nullptr) {
     int rc = require_device(c);
     if (rc) return rc;
     if ((rc = check_layer(c, layer))) return rc;
@@ -1161,8 +1173,60 @@ static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *g
         a.min_pages = kMinPagesPerWg;
     }
     a.out = static_cast<uint16_t *>(out);
+    if (app) {
+        kva::AppendArgs ap = *app;
+        ap.keep_k = 1;
+        if (a.whole) {
+            a.fused = 1;
+            a.app = ap;
+        } else {
+            KVA_HIP(kva::launch_append(ap, static_cast<hipStream_t>(stream)));
+        }
+    }
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;
+}
+
+static int append_decode_impl(kva_cache *c, int32_t layer, void *q, const void *k, const void *v,
+                              const void *q_norm_w, const void *k_norm_w, const void *cos_tab, const void *sin_tab,
+                              int32_t table_rows, const void *gate, int64_t gate_stride, void *out,
+                              kva_stream_t stream) {
+    int rc = require_device(c);
+    if (rc) return rc;
+    if ((rc = check_layer(c, layer))) return rc;
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    if (!c->st_all_one) return fail(KVA_ERR_STATE, "kva_append_decode needs exactly one new token per sequence");
+    kva::AppendArgs ap;
+    if ((rc = make_append(c, layer, q, const_cast<void *>(k), v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows,
+                          ap)))
+        return rc;
+    return decode_impl(c, layer, q, gate, gate_stride, out, stream, &ap);
+}
+
+int kva_append_decode(kva_cache *c, int32_t layer, void *q, const void *k, const void *v, const void *q_norm_w,
+                      const void *k_norm_w, const void *cos_tab, const void *sin_tab, int32_t table_rows, void *out,
+                      kva_stream_t stream) {
+    int rc = capture_check(c, stream);
+    if (rc) return capture_note(c, rc);
+    rc = append_decode_impl(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, nullptr, 0, out,
+                            stream);
+    if (rc == KVA_OK && c->capturing)
+        c->cap_table_rows = c->cap_table_rows ? std::min(c->cap_table_rows, table_rows) : table_rows;
+    return capture_note(c, rc);
+}
+
+int kva_append_decode_gated(kva_cache *c, int32_t layer, void *q, const void *k, const void *v,
+                            const void *q_norm_w, const void *k_norm_w, const void *cos_tab, const void *sin_tab,
+                            int32_t table_rows, const void *gate, int64_t gate_stride, void *out,
+                            kva_stream_t stream) {
+    int rc = capture_check(c, stream);
+    if (rc) return capture_note(c, rc);
+    if (!gate) return capture_note(c, fail(KVA_ERR_INVALID_ARG, "NULL gate"));
+    rc = append_decode_impl(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, gate, gate_stride,
+                            out, stream);
+    if (rc == KVA_OK && c->capturing)
+        c->cap_table_rows = c->cap_table_rows ? std::min(c->cap_table_rows, table_rows) : table_rows;
+    return capture_note(c, rc);
 }
 
 int kva_append_qknorm_rope(kva_cache *c, int32_t layer, void *q, void *k, const void *v,

@@ -36,6 +36,7 @@ struct AppendArgs {
     int32_t num_kv_heads;
     int32_t half_rot;
     float eps;
+    int32_t keep_k;           // 1: k is read only (the cache gets the normalised rows)
 };
 hipError_t launch_append(const AppendArgs &a, hipStream_t s);
 
@@ -151,6 +152,14 @@ struct DecodeArgs {
     // of G / whole query heads): no partials, no combine; the stream-K
     // fields are unused.  G / whole must be 1, 2, 3, 4, 6 or 8.
     int32_t whole;
+    // 1 (whole form only): the step's append is done in the same launch
+    // from `app` (one new token per sequence, token b of sequence b): each
+    // workgroup normalises and rotates its query rows (written back in
+    // place, q = app.q) and its kv head's new K row, the first group of each
+    // (sequence, kv head) writes the new K and V rows to the cache, and the
+    // new token joins the attention from registers, not from the cache.
+    int32_t fused;
+    AppendArgs app;
 };
 constexpr int kTimelineWords = 4;
 constexpr int kWholeWaves = 8;  // waves per whole-sequence decode workgroup

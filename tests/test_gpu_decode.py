@@ -267,3 +267,79 @@ def test_decode_c3_full_workload(device):
     print(f"c3 max err {err:.2e} split {split} x {ns}")
     assert err <= TOL
     cache.destroy()
+
+
+@pytest.mark.parametrize("longest", [1000, 3000])
+def test_append_decode_matches_append_then_decode(device, longest):
+    """kva_append_decode (one launch in the whole-sequence form, longest
+    1000; append + stream-K decode past 1024 rows, longest 3000) against
+    kva_append_qknorm_rope + kva_decode on a twin cache: the pools and the
+    normalised q bit-identical, k left as given, both outputs within 2e-3 of
+    the oracle.  A second step runs ungated on one cache and gated on the
+    other: the gated output within one fp16 ulp of the oracle gate applied to
+    the ungated one, and within 2e-3 of the gated oracle attention."""
+    lengths = [0, 1, 14, 15, 16, 17, 100, 255, longest]
+    nblk = [(L + 2 + 15) // 16 for L in lengths]
+    perm = np.random.default_rng(41).permutation(sum(nblk))
+    ids, o = [], 0
+    for n in nblk:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say(f"append+decode fused longest={longest}")
+    fused, kr, vr = build_cache(lengths, ids, extra_rows=2, rng=np.random.default_rng(42))
+    twin, _, _ = build_cache(lengths, ids, extra_rows=2, rng=np.random.default_rng(42))
+    rng = np.random.default_rng(43)
+    B = len(lengths)
+    q = rng.standard_normal((B, H, D), dtype=np.float32).astype(np.float16)
+    k = rng.standard_normal((B, HKV, D), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((B, HKV, D), dtype=np.float32).astype(np.float16)
+    gate = (2 * rng.standard_normal((B, H, D), dtype=np.float32)).astype(np.float16)
+    qw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    kw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    tables = Tables(device, 4096)
+    dqw, dkw, dv = device.array(qw), device.array(kw), device.array(v)
+    dq_f, dk_f = device.array(q), device.array(k)
+    dq_t, dk_t = device.array(q), device.array(k)
+    out_f, out_t = device.empty((B, H, D), np.float16), device.empty((B, H, D), np.float16)
+    for c in (fused, twin):
+        c.begin_step(list(range(B)), [1] * B)
+    fused.append_decode(0, dq_f, dk_f, dv, dqw, dkw, tables.d_cos, tables.d_sin, tables.rows, out_f)
+    twin.append(0, dq_t, dk_t, dv, dqw, dkw, tables.d_cos, tables.d_sin, tables.rows)
+    twin.decode(0, dq_t, out_t)
+    device.synchronize()
+    assert (fused.decode_split()[0] == 0) == (longest <= 1024)  # whole-sequence form: one launch
+    for a, b in zip(fused.download_pools(0), twin.download_pools(0)):
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    assert np.array_equal(dq_f.numpy().view(np.uint16), dq_t.numpy().view(np.uint16))
+    assert np.array_equal(dk_f.numpy().view(np.uint16), k.view(np.uint16))
+    pos = np.asarray(lengths)
+    qn, kn = expected_norm(q, qw, tables, pos), expected_norm(k, kw, tables, pos)
+    ks = [np.concatenate([kr[0][b], kn[b:b + 1]]) for b in range(B)]
+    vs = [np.concatenate([vr[0][b], v[b:b + 1]]) for b in range(B)]
+    exp = orc.decode_attention(qn, ks, vs)
+    assert max_err(out_f.numpy(), exp) <= TOL
+    assert max_err(out_t.numpy(), exp) <= TOL
+    # No cached row before the step: the output is the new V row exactly.
+    assert np.array_equal(out_f.numpy()[0].view(np.uint16), np.repeat(v[:1], H // HKV, 1)[0].view(np.uint16))
+
+    # Second step (same inputs at the next position): ungated on one cache, gated on the other.
+    dq_u, dq_g, dgate = device.array(q), device.array(q), device.array(gate)
+    out_u, out_g = device.empty((B, H, D), np.float16), device.empty((B, H, D), np.float16)
+    for c in (fused, twin):
+        c.begin_step(list(range(B)), [1] * B)
+    fused.append_decode(0, dq_u, dk_f, dv, dqw, dkw, tables.d_cos, tables.d_sin, tables.rows, out_u)
+    twin.append_decode(0, dq_g, dk_f, dv, dqw, dkw, tables.d_cos, tables.d_sin, tables.rows, out_g, gate=dgate)
+    device.synchronize()
+    u, g = out_u.numpy(), out_g.numpy()
+    ordered = lambda x: np.where(x.view(np.uint16) & 0x8000, -(x.view(np.uint16).astype(np.int32) & 0x7FFF),
+                                 x.view(np.uint16).astype(np.int32))
+    assert np.abs(ordered(g) - ordered(orc.sigmoid_gate(u, gate))).max() <= 1
+    pos2 = pos + 1
+    qn2, kn2 = expected_norm(q, qw, tables, pos2), expected_norm(k, kw, tables, pos2)
+    ks2 = [np.concatenate([ks[b], kn2[b:b + 1]]) for b in range(B)]
+    vs2 = [np.concatenate([vs[b], v[b:b + 1]]) for b in range(B)]
+    exp2 = orc.decode_attention(qn2, ks2, vs2)
+    assert max_err(u, exp2) <= TOL
+    assert max_err(g, orc.sigmoid_gate(exp2.astype(np.float16), gate)) <= TOL
+    for c in (fused, twin):
+        c.destroy()
