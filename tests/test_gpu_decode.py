@@ -343,3 +343,74 @@ def test_append_decode_matches_append_then_decode(device, longest):
     assert max_err(g, orc.sigmoid_gate(exp2.astype(np.float16), gate)) <= TOL
     for c in (fused, twin):
         c.destroy()
+
+
+@pytest.mark.parametrize("h,hkv,B,L", [(24, 4, 64, 100), (24, 4, 24, 333), (24, 4, 16, 700), (32, 4, 64, 100),
+                                       (32, 4, 32, 1000), (16, 4, 64, 64), (16, 4, 32, 1024), (8, 2, 3, 17)])
+def test_whole_form_head_groups(device, h, hkv, B, L):
+    """The whole-sequence form at every query-head group width it launches
+    (G / workgroups per kv head = 1, 2, 3, 4, 6, 8 across these shapes),
+    through kva_legacy_decode_batched without a workspace: contiguous K/V of
+    B sequences of L rows each, within 2e-3 of the fp32 oracle."""
+    rng = np.random.default_rng(60 + h + B + L)
+    stride_rows = L + 3
+    K = rng.standard_normal((B, stride_rows, hkv, D), dtype=np.float32).astype(np.float16)
+    V = rng.standard_normal((B, stride_rows, hkv, D), dtype=np.float32).astype(np.float16)
+    Q = rng.standard_normal((B, h, D), dtype=np.float32).astype(np.float16)
+    say(f"whole form h={h} hkv={hkv} B={B} L={L}")
+    dq, dk, dv = device.array(Q), device.array(K), device.array(V)
+    out = device.empty((B, h, D), np.float16)
+    _lib.call("kva_legacy_decode_batched", None, dq.ptr, dk.ptr, dv.ptr, out.ptr, L, B,
+              stride_rows * hkv * D * 2, h, hkv, None)
+    device.synchronize()
+    ref = np.stack([orc.attention_fp32(Q[b:b + 1], K[b, :L], V[b, :L])[0] for b in range(B)])
+    assert max_err(out.numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("B", [16, 32, 64])
+def test_append_decode_head_groups(device, B):
+    """kva_append_decode with 2, 3 and 6 query heads per workgroup (B = 16,
+    32, 64 sequences of 24 q / 4 kv heads on 256 CUs): cache rows and q
+    bit-identical to append + decode on a twin cache, output within 2e-3 of
+    the oracle."""
+    rng = np.random.default_rng(70 + B)
+    lengths = [int(x) for x in rng.integers(0, 200, B)]
+    nblk = [(n + 1 + 15) // 16 for n in lengths]
+    perm = rng.permutation(sum(nblk))
+    ids, o = [], 0
+    for n in nblk:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say(f"append+decode head groups B={B}")
+    fused, kr, vr = build_cache(lengths, ids, extra_rows=1, rng=np.random.default_rng(71))
+    twin, _, _ = build_cache(lengths, ids, extra_rows=1, rng=np.random.default_rng(71))
+    q = rng.standard_normal((B, H, D), dtype=np.float32).astype(np.float16)
+    k = rng.standard_normal((B, HKV, D), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((B, HKV, D), dtype=np.float32).astype(np.float16)
+    qw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    kw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    tables = Tables(device, 256)
+    dqw, dkw, dv = device.array(qw), device.array(kw), device.array(v)
+    dq_f, dq_t, dk = device.array(q), device.array(q), device.array(k)
+    dk_t = device.array(k)
+    out_f, out_t = device.empty((B, H, D), np.float16), device.empty((B, H, D), np.float16)
+    for c in (fused, twin):
+        c.begin_step(list(range(B)), [1] * B)
+    fused.append_decode(0, dq_f, dk, dv, dqw, dkw, tables.d_cos, tables.d_sin, tables.rows, out_f)
+    twin.append(0, dq_t, dk_t, dv, dqw, dkw, tables.d_cos, tables.d_sin, tables.rows)
+    twin.decode(0, dq_t, out_t)
+    device.synchronize()
+    used, n_wg = fused.decode_split()
+    assert used == 0 and n_wg % (B * HKV) == 0
+    for a, b in zip(fused.download_pools(0), twin.download_pools(0)):
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    assert np.array_equal(dq_f.numpy().view(np.uint16), dq_t.numpy().view(np.uint16))
+    pos = np.asarray(lengths)
+    qn, kn = expected_norm(q, qw, tables, pos), expected_norm(k, kw, tables, pos)
+    ks = [np.concatenate([kr[0][b], kn[b:b + 1]]) for b in range(B)]
+    vs = [np.concatenate([vr[0][b], v[b:b + 1]]) for b in range(B)]
+    exp = orc.decode_attention(qn, ks, vs)
+    assert max_err(out_f.numpy(), exp) <= TOL
+    assert max_err(out_t.numpy(), exp) <= TOL
+    for c in (fused, twin):
+        c.destroy()
