@@ -42,7 +42,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from mi50grad_amd import _lib  # noqa: E402
-from mi50grad_amd.device import Event, GPUDevice, Stream  # noqa: E402
+from mi50grad_amd.device import Event, GPUDevice, Stream, device_props  # noqa: E402
 from mi50grad_amd.kv_cache import PagedKVCache  # noqa: E402
 from mi50grad_amd.rope import rope_tables  # noqa: E402
 from mi50grad_amd import workloads as wl  # noqa: E402
@@ -539,6 +539,27 @@ def c2_workload(dev, steps_unused, warmup, graph=False, split=0, fused=True):
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
 
 
+def mfma_peak_derived() -> dict:
+    """Dense fp16 MFMA peak from this device's CU count and peak clock: a
+    v_mfma_f32_16x16x32_f16 does 16384 FLOPs in 16 cycles on each of a CU's
+    4 SIMDs, 4096 FLOPs per CU per clock."""
+    p = device_props()
+    return {"tflops": p["n_cu"] * p["clock_khz"] * 1e3 * 4096 / 1e12, "n_cu": p["n_cu"],
+            "clock_mhz": p["clock_khz"] / 1e3,
+            "method": "kva_dev_props: CUs x peak shader clock x 4096 dense fp16 FLOP per CU per clock"}
+
+
+def stored_mfma_busy() -> dict | None:
+    """MFMA-busy fraction of the prefill kernel from its stored rocprofv3
+    counter profile (not counted in this run)."""
+    path = ROOT / "profiles" / "prefill_c4_mfma.json"
+    if not path.exists():
+        return None
+    d = json.loads(path.read_text())["derived"]
+    return {"fraction": d["mfma_busy_fraction"], "source": "profiles/prefill_c4_mfma.json: "
+            "SQ_VALU_MFMA_BUSY_CYCLES per SIMD over the kernel's cycles (a stored profile)"}
+
+
 def c4_workload(dev, steps, warmup):
     """Config 4: 4 sequences append a 512-token chunk after 0/256/1024/2048
     cached rows (fused norm+RoPE+append), then causal prefill attention; 16
@@ -854,6 +875,8 @@ def main() -> int:
                           "kv_gbs": r["kv_bytes"] / r["steps"] / (r["step_us"] * 1e-6) / 1e9,
                           "back_to_back_us_per_step": warm_us, "dtype": "f16",
                           "data": "synthetic",
+                          "launches_per_step": {"kernels": LAYERS, "plan_copies": 1,
+                                                "two_calls_kernels": 2 * LAYERS},
                           "two_calls_per_layer": {"step_us": r2["step_us"],
                                                   "back_to_back_us_per_step": r2["wall_s"] * 1e6 / r2["steps"],
                                                   "calls": "kva_append_qknorm_rope + kva_decode"},
@@ -914,7 +937,8 @@ def main() -> int:
                          "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("prefill_c4_traffic.json"),
                          "kernel": "kva_prefill = mq_kernel<1 tile, 8 waves, causal> + mq_combine_kernel",
                          "avg_us": r["prefill_avg_us"], "alg_flops_per_launch": r["flops_per_layer"],
-                         "alg_bytes_per_launch": r["bytes_per_layer"]}}))
+                         "alg_bytes_per_launch": r["bytes_per_layer"], "mfma_busy": stored_mfma_busy(),
+                         "peak_derived": mfma_peak_derived()}}))
         return 0
     if args.workload == "c5":
         r = c5_workload(dev, args.steps, args.warmup)

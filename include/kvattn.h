@@ -396,6 +396,12 @@ int kva_hbm_read(const void *src, size_t bytes, void *sink, kva_stream_t stream)
 
 /* ---- device helpers (the GPUDevice surface, hip_dispatch.py:594-703) ----- */
 int kva_dev_count(int32_t *n);
+/* The current device's compute units, peak shader clock (kHz), memory clock
+ * (kHz) and memory bus width (bits), from hipGetDeviceProperties: what a
+ * bench derives its peaks from next to the vendor figures.  No reference
+ * counterpart (its benchmarks quote fixed MI50 peaks).                     */
+int kva_dev_props(int32_t *n_cu, int32_t *clock_khz, int32_t *mem_clock_khz,
+                  int32_t *mem_bus_bits);
 int kva_dev_set(int32_t device);
 int kva_dev_malloc(void **ptr, size_t bytes);
 int kva_dev_free(void *ptr);

@@ -95,6 +95,7 @@ SIGNATURES = {
     "kva_hbm_copy": [_P, _P, c_size_t, _P],
     "kva_hbm_read": [_P, c_size_t, _P, _P],
     "kva_dev_count": [_PI],
+    "kva_dev_props": [_PI, _PI, _PI, _PI],
     "kva_dev_set": [_I],
     "kva_dev_malloc": [POINTER(c_void_p), c_size_t],
     "kva_dev_free": [_P],

@@ -1688,6 +1688,18 @@ int kva_dev_count(int32_t *n) {
     *n = c;
     return KVA_OK;
 }
+int kva_dev_props(int32_t *n_cu, int32_t *clock_khz, int32_t *mem_clock_khz, int32_t *mem_bus_bits) {
+    if (!n_cu || !clock_khz || !mem_clock_khz || !mem_bus_bits) return fail(KVA_ERR_INVALID_ARG, "NULL argument");
+    int dev = 0;
+    KVA_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t p{};
+    KVA_HIP(hipGetDeviceProperties(&p, dev));
+    *n_cu = p.multiProcessorCount;
+    *clock_khz = p.clockRate;
+    *mem_clock_khz = p.memoryClockRate;
+    *mem_bus_bits = p.memoryBusWidth;
+    return KVA_OK;
+}
 int kva_dev_set(int32_t d) {
     KVA_HIP(hipSetDevice(d));
     return KVA_OK;

@@ -154,3 +154,11 @@ def device_count() -> int:
     n = ctypes.c_int32()
     _lib.call("kva_dev_count", ctypes.byref(n))
     return n.value
+
+
+def device_props() -> dict:
+    """Compute units, peak shader clock, memory clock (kHz) and memory bus
+    width (bits) of the current device (kva_dev_props)."""
+    v = [ctypes.c_int32() for _ in range(4)]
+    _lib.call("kva_dev_props", *[ctypes.byref(x) for x in v])
+    return {"n_cu": v[0].value, "clock_khz": v[1].value, "mem_clock_khz": v[2].value, "mem_bus_bits": v[3].value}
