@@ -17,6 +17,10 @@ decode kernel alone: algorithmic bytes per launch (KV rows read + queries)
 over its average duration from HIP events recorded on the launch stream
 around each decode launch inside the timed region.  ``cpu_baseline`` is the
 numpy oracle on a bounded sample of the same workload on this host.
+The default line also carries the fixed ctx=8192 case (``ctx8192``), the
+measured read and copy ceilings (``peaks``) and every other workload's own
+figures (``other_configs``: c1, c2, c4, c5, proj, proj4); --no-extras drops
+those three.
 
 Other workloads: --workload c1 (the one-layer config-1 step: GPU latency
 next to the numpy oracle's, 1 and all BLAS threads), ctx8192 (every
@@ -24,8 +28,9 @@ sequence at 8192 rows), c2
 (16 layers, B=1, 128 decode steps growing 128 -> 256 rows), c2graph (the
 same with the 16-layer step recorded once and replayed), c4 (chunked
 prefill), c5 (tree verify + rollback), proj (config 3 with its producer:
-the fused Q/K/V projection + append, then the gated decode), copy (HBM
-stream-copy probe: the measured bandwidth ceiling).
+the fused Q/K/V projection + append, then the gated decode), proj4 (the
+config-4 producer: 2048 tokens through the library GEMM), copy and read
+(HBM stream probes: the measured bandwidth ceilings).
 """
 from __future__ import annotations
 
@@ -818,36 +823,17 @@ def load_traffic(name: str):
         return None
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "proj4", "copy", "read"])
-    ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extras", action="store_true",
-                    help="c3: leave out the ctx8192 variant and the bandwidth probes")
-    ap.add_argument("--timeline", action="store_true",
-                    help="c3/ctx8192: after the timed steps, record the decode kernels' per-workgroup "
-                         "timeline (kva_timeline_enable) for one more step and add its summary")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build runs the path on a single MI355X "
-              "(see the sharding design); run it with --gpus 1", file=sys.stderr)
-        return 2
-    dev = GPUDevice(0)
-
+def workload_line(dev, args) -> dict:
+    """The bench line (a dict) of every workload but the decode ones."""
     if args.workload in ("copy", "read"):
         r = copy_probe(dev) if args.workload == "copy" else read_probe(dev)
-        print(json.dumps({"metric": f"HBM stream {args.workload} GB/s", "value": r["gbs"], "unit": "GB/s",
+        return ({"metric": f"HBM stream {args.workload} GB/s", "value": r["gbs"], "unit": "GB/s",
                           "n_gpus": 1, "avg_us": r["avg_us"], "bytes_per_launch": r["bytes_per_launch"],
-                          "higher_is_better": True}))
-        return 0
+                          "higher_is_better": True})
     if args.workload == "c1":
         r = c1_workload(dev)
         by = 256 * ROW_BYTES + 2 * H * D * 2 + 2 * HKV * D * 2
-        print(json.dumps({
+        return ({
             "metric": "config-1 one-layer step latency (append at 255 + decode over 256, B=1)",
             "value": r["gpu_us"], "unit": "us", "n_gpus": 1, "steps": r["reps"], "higher_is_better": False,
             "dtype": "f16", "data": "synthetic (seed 0, the config-1 recipe)",
@@ -858,15 +844,14 @@ def main() -> int:
                              "all_threads_us": r["cpu_us_all"], "host_logical_cpus": os.cpu_count(),
                              "cpu_model": _cpu_model(),
                              "sample": "the whole config-1 step in the numpy oracle, median of 25 calls, "
-                                       "1 BLAS thread (value) and all BLAS threads"}}))
-        return 0
+                                       "1 BLAS thread (value) and all BLAS threads"}})
     if args.workload in ("c2", "c2graph"):
         graph = args.workload == "c2graph"
         r = c2_workload(dev, args.steps, args.warmup, graph=graph, split=args.split)
         r2 = c2_workload(dev, args.steps, args.warmup, graph=graph, split=args.split, fused=False)
         ms = r["step_us"] * 1e-3
         warm_us = r["wall_s"] * 1e6 / r["steps"]
-        print(json.dumps({"metric": "config-2 decode step time (16 layers, B=1, 128->256 rows)",
+        return ({"metric": "config-2 decode step time (16 layers, B=1, 128->256 rows)",
                           "value": r["step_us"], "unit": "us/step", "n_gpus": 1, "steps": r["steps"],
                           "ms_per_step": ms, "higher_is_better": False,
                           "timing": "HIP events around each step (plan upload + 16 layers) on the launch "
@@ -881,14 +866,13 @@ def main() -> int:
                                                   "back_to_back_us_per_step": r2["wall_s"] * 1e6 / r2["steps"],
                                                   "calls": "kva_append_qknorm_rope + kva_decode"},
                           "config": {"workload": "C2", "calls": "kva_append_decode per layer",
-                                     "dispatch": "recorded step replay" if graph else "per-layer calls"}}))
-        return 0
+                                     "dispatch": "recorded step replay" if graph else "per-layer calls"}})
 
     if args.workload == "proj":
         r = proj_workload(dev, args.steps, args.warmup)
         gbs = r["alg_bytes_proj"] / (r["proj_avg_us"] * 1e-6) / 1e9
         ms = r["wall_s"] * 1e3 / r["steps"]
-        print(json.dumps({
+        return ({
             "metric": "config-3 producer GB/s: fused Q/K/V projection + norm + RoPE + append (B=32, hidden 5120)",
             "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
@@ -903,14 +887,13 @@ def main() -> int:
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("project_c3_traffic.json"),
                          "kernel": "kva_project_append = proj_lds_kernel<2 token tiles, 8 waves, 7 row tiles, "
                                    "10 k-steps, 6 stages> + proj_finish_kernel",
-                         "avg_us": r["proj_avg_us"], "alg_bytes_per_launch": r["alg_bytes_proj"]}}))
-        return 0
+                         "avg_us": r["proj_avg_us"], "alg_bytes_per_launch": r["alg_bytes_proj"]}})
     if args.workload == "proj4":
         r = proj_prefill_workload(dev, args.steps, args.warmup)
         us = r["proj_avg_us"]
         tflops = r["flops"] / (us * 1e-6) / 1e12
         alg = r["weight_bytes"] + r["tokens"] * r["hidden"] * 2 + 2 * r["tokens"] * (H + HKV) * D * 2
-        print(json.dumps({
+        return ({
             "metric": "config-4 producer: kva_project_append of 2048 tokens from hidden 5120 (norm + RoPE + append)",
             "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
             "ms_per_step": r["wall_s"] * 1e3 / r["steps"], "higher_is_better": True, "dtype": "f16",
@@ -920,14 +903,13 @@ def main() -> int:
             "alg_bytes_per_layer": alg, "weights_gbs": r["weight_bytes"] / (us * 1e-6) / 1e9,
             "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("project_c4_traffic.json"),
-                         "avg_us": us, "alg_flops_per_launch": r["flops"]}}))
-        return 0
+                         "avg_us": us, "alg_flops_per_launch": r["flops"]}})
     if args.workload == "c4":
         r = c4_workload(dev, args.steps, args.warmup)
         tflops = r["flops_per_layer"] / (r["prefill_avg_us"] * 1e-6) / 1e12
         ms = r["wall_s"] * 1e3 / r["steps"]
         extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c4()}
-        print(json.dumps({**extra, 
+        return ({**extra, 
             "metric": "config-4 chunked prefill attention TFLOP/s (pp512 after 0/256/1024/2048 rows, B=4)",
             "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
@@ -938,14 +920,13 @@ def main() -> int:
                          "kernel": "kva_prefill = mq_kernel<1 tile, 8 waves, causal> + mq_combine_kernel",
                          "avg_us": r["prefill_avg_us"], "alg_flops_per_launch": r["flops_per_layer"],
                          "alg_bytes_per_launch": r["bytes_per_layer"], "mfma_busy": stored_mfma_busy(),
-                         "peak_derived": mfma_peak_derived()}}))
-        return 0
+                         "peak_derived": mfma_peak_derived()}})
     if args.workload == "c5":
         r = c5_workload(dev, args.steps, args.warmup)
         gbs = r["alg_bytes_per_layer"] / (r["verify_avg_us"] * 1e-6) / 1e9
         ms = r["wall_s"] * 1e3 / r["steps"]
         extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c5()}
-        print(json.dumps({**extra, 
+        return ({**extra, 
             "metric": "config-5 tree-verify attention GB/s (B=64, ctx U[4096,32768], 9-node tree)",
             "value": gbs, "unit": "GB/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
@@ -954,7 +935,32 @@ def main() -> int:
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("tree_c5_traffic.json"),
                          "kernel": "kva_tree_verify = mq_kernel<1 tile, 4 waves, tree> + mq_combine_kernel",
-                         "avg_us": r["verify_avg_us"], "alg_bytes_per_launch": r["alg_bytes_per_layer"]}}))
+                         "avg_us": r["verify_avg_us"], "alg_bytes_per_launch": r["alg_bytes_per_layer"]}})
+    raise ValueError(args.workload)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "proj4", "copy", "read"])
+    ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="c3: leave out the ctx8192 variant, the bandwidth probes and the other configs")
+    ap.add_argument("--timeline", action="store_true",
+                    help="c3/ctx8192: after the timed steps, record the decode kernels' per-workgroup "
+                         "timeline (kva_timeline_enable) for one more step and add its summary")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build runs the path on a single MI355X "
+              "(see the sharding design); run it with --gpus 1", file=sys.stderr)
+        return 2
+    dev = GPUDevice(0)
+
+    if args.workload not in ("c3", "ctx8192"):
+        print(json.dumps(workload_line(dev, args)), flush=True)
         return 0
     line = decode_line(dev, args.workload, args)
     if args.workload == "c3" and not args.no_extras:
@@ -973,11 +979,41 @@ def main() -> int:
             "method": "kva_hbm_read over 4 GiB (read-only: 2048 contiguous shares, two passes of 4 x 16-byte loads per lane in flight) and "
                       "kva_hbm_copy over 4 GiB (bytes read + written), averages of 20 launches between "
                       "HIP events; roofline.frac stays against the vendor 8 TB/s"}
+    if args.workload == "c3" and not args.no_extras:
+        line["other_configs"] = other_configs(dev, args)
     if not args.no_cpu_baseline:
         log("cpu baseline (numpy oracle, ~10 s at 1 thread + ~10 s at all threads)")
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
     return 0
+
+
+def other_configs(dev, args) -> dict:
+    """The other configs' figures in the default line (each workload's own
+    line, the CPU baselines left out), so one default run records them all."""
+    pick = {
+        "c1": lambda d: {"us_per_step": d["value"], "two_calls_us": d["two_calls_us"],
+                         "gpu_min_us": d["gpu_min_us"], "calls": d["config"]["calls"]},
+        "c2": lambda d: {"us_per_step": d["value"], "back_to_back_us_per_step": d["back_to_back_us_per_step"],
+                         "two_calls_us_per_step": d["two_calls_per_layer"]["step_us"],
+                         "launches_per_step": d["launches_per_step"], "timing": d["timing"]},
+        "c4": lambda d: {"tflops": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
+                         "tok_per_s": d["tok_per_s"], "mfma_busy": d["roofline"]["mfma_busy"]},
+        "c5": lambda d: {"gbs": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
+                         "rollback_avg_us": d["rollback_avg_us"]},
+        "proj": lambda d: {"gbs": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
+                           "out_project_avg_us": d["out_project"]["avg_us"],
+                           "out_project_gbs": d["out_project"]["gbs"]},
+        "proj4": lambda d: {"tflops": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
+                            "path": d["path"]},
+    }
+    out = {}
+    for w, f in pick.items():
+        log(f"other config {w}")
+        sub = argparse.Namespace(**{**vars(args), "workload": w, "no_cpu_baseline": True})
+        d = workload_line(dev, sub)
+        out[w] = {"metric": d["metric"], "unit": d["unit"], **f(d)}
+    return out
 
 
 def decode_line(dev, which, args):
