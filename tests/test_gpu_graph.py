@@ -42,9 +42,13 @@ def _twin(lengths, split, seed):
     return caches, hist
 
 
-@pytest.mark.parametrize("lengths,split", [([14, 30], 0), ([200, 5, 77], 32)])
-def test_graph_replay_matches_eager(device, lengths, split):
-    say(f"graph replay lengths={lengths} split={split}")
+@pytest.mark.parametrize("lengths,split,fused", [([14, 30], 0, False), ([200, 5, 77], 32, False),
+                                                 ([14, 30], 0, True), ([200, 5, 77], 32, True)])
+def test_graph_replay_matches_eager(device, lengths, split, fused):
+    """fused: each layer is one kva_append_decode call (a single launch in
+    the whole-sequence form at the automatic split; append + stream-K decode
+    with the split set), recorded and replayed like the two-call form."""
+    say(f"graph replay lengths={lengths} split={split} fused={fused}")
     rng = np.random.default_rng(5)
     (eager, graphed), hist = _twin(lengths, split, seed=11)
     B = len(lengths)
@@ -76,6 +80,10 @@ def test_graph_replay_matches_eager(device, lengths, split):
     def calls(cache, which, stream_h):
         for layer in range(LAYERS):
             b = bufs[which][layer]
+            if fused:
+                cache.append_decode(layer, b["q"], b["k"], b["v"], qw[layer], kw[layer], tables.d_cos,
+                                    tables.d_sin, tables.rows, b["out"], stream=stream_h)
+                continue
             cache.append(layer, b["q"], b["k"], b["v"], qw[layer], kw[layer], tables.d_cos, tables.d_sin,
                          tables.rows, stream=stream_h)
             cache.decode(layer, b["q"], b["out"], stream=stream_h)
