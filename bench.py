@@ -120,7 +120,8 @@ def timeline_summary(rec: np.ndarray) -> dict:
     [n_wg, rows, 8 waves, 4]): per workgroup, entry = first wave's entry,
     first issue = when its first K/V loads were out, end = its last wave's
     walk end; microseconds (100 MHz ticks)."""
-    ent = rec[:, :, :, 0].min(axis=(1, 2))
+    ran = rec[:, :, :, 0] > 0  # waves a workgroup does not have leave zero records
+    ent = np.where(ran, rec[:, :, :, 0], np.iinfo(np.int64).max).min(axis=(1, 2))
     first = rec[:, :, :, 1].max(axis=(1, 2))
     end = rec[:, :, :, 2].max(axis=(1, 2))
     xcd = (rec[:, 0, 0, 3] >> 32) & 0xF
@@ -1056,7 +1057,7 @@ def decode_line(dev, which, args):
                      "traffic_source": f"profiles/{traffic_file}: rocprofv3 FETCH_SIZE and WRITE_SIZE of this "
                                        "workload (separate runs), scaled by the copy-kernel calibration stored "
                                        "there; a stored figure, not counted in this run",
-                     "kernel": "kva_decode = decode_kernel<6> (stream-K) + combine_kernel<6> (one stream, "
+                     "kernel": "kva_decode = decode_mfma_kernel<6> (stream-K, QK on MFMA) + combine_kernel<6> (one stream, "
                                "HIP events around the call)",
                      "avg_us": r["decode_avg_us"],
                      "alg_bytes_per_launch": r["alg_bytes_decode_launch"]},

@@ -299,10 +299,11 @@ int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,
  * GPU's constant clock), and the XCD (bits 32-35) with the workgroup's page
  * count (bits 0-31).  kva_timeline_read copies the last decode's records,
  * [n_wg][grid_rows][8 waves][4] words (a synchronising call); the recorded
- * workload is otherwise unchanged.  A decode in the whole-sequence form
- * records its workgroups (n_wg of them, grid_rows = 1; several per sequence
- * and kv head), each with its sequence's page count.  Off by default; costs one device buffer
- * while on.                                                                 */
+ * workload is otherwise unchanged.  The stream-K decode runs one wave per kv
+ * head: the records of waves a workgroup does not have are zero.  A decode
+ * in the whole-sequence form records its workgroups (n_wg of them,
+ * grid_rows = 1; several per sequence and kv head), each with its
+ * sequence's page count.  Off by default; costs one device buffer while on. */
 int kva_timeline_enable(kva_cache *cache, int32_t on);
 int kva_timeline_read(const kva_cache *cache, uint64_t *dst, size_t cap_words,
                       int32_t *n_wg, int32_t *grid_rows);

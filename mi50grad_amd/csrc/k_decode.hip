@@ -562,6 +562,326 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
     }
 }
 
+// ---- Stream-K decode with QK on the matrix cores ----
+//
+// The same page split, partial slots and combine as decode_kernel, with one
+// wave per kv head walking every page of the workgroup's range (16 token
+// rows a step) and no cross-wave merge.
+//   QK: S^T = K Q^T on v_mfma_f32_16x16x32_f16, the page's 16 rows as the A
+//       operand and the G query rows as columns 0..G-1 of B (the others
+//       zero).  The k order inside the product is free as long as A and B
+//       agree, so lane group g's k-step s covers dims 64g + 8s .. +7: each
+//       lane loads its row's 128 contiguous bytes, dims 64g .. 64g+63.
+//   softmax: on the C layout (lane: head column l%16, rows 4(l/16)..+3);
+//       the column max over the four lane groups by permlane swaps.
+//   PV: the fp16 probability pairs go through 64 dwords of LDS per wave
+//       ([token pair][head]) to every lane, which folds token pairs with
+//       v_dot2_f32_f16 into dims 4l..4l+3 of every head, as decode_kernel.
+constexpr int kMfmaWaves = kDecodeHeadsPerWg;  // waves (kv heads) per workgroup, at most
+
+struct Page {
+    uint4 k[8];   // this lane's row (l%16), dims 64(l/16) .. +63
+    uint2 v[16];  // rows 0..15, dims 4l .. 4l+3
+};
+
+__device__ __forceinline__ void load_page(Page &p, const char *kb, const char *vb, int lim, bool on, uint32_t koff,
+                                          uint32_t voff, int row_bytes) {
+    const uint32_t n = on ? static_cast<uint32_t>(lim * row_bytes) : 0u;
+    const auto rk = page_rsrc(kb, n), rv = page_rsrc(vb, n);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * s, 0, 0);
+        p.k[s] = make_uint4(x[0], x[1], x[2], x[3]);
+    }
+#pragma unroll
+    for (int t = 0; t < kBlockTokens; ++t) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + t * row_bytes, 0, 0);
+        p.v[t] = make_uint2(x[0], x[1]);
+    }
+}
+
+__device__ __forceinline__ void consume(const Page &p) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) asm volatile("" ::"v"(p.k[s].x), "v"(p.k[s].y), "v"(p.k[s].z), "v"(p.k[s].w));
+#pragma unroll
+    for (int t = 0; t < kBlockTokens; ++t) asm volatile("" ::"v"(p.v[t].x), "v"(p.v[t].y));
+}
+
+// m: the running max of this lane's head column (raw scores), l: the fp16
+// probabilities of this lane's four rows summed, acc: dims 4l..4l+3 of every
+// head of the group.
+template <int G>
+struct MfmaState {
+    float m, l, acc[G][4];
+};
+
+template <int G>
+__device__ __forceinline__ void reset(MfmaState<G> &st) {
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) st.acc[g][c] = 0.0f;
+}
+
+// Fold a page into the state; rows >= lim are masked (lim >= 1).  qb: the B
+// operand (this lane's column: query head l%16, zero past G).
+template <int G>
+__device__ __forceinline__ void compute_page(MfmaState<G> &st, const Page &p, const uint4 (&qb)[8], int lane, int lim,
+                                             uint32_t *pbuf) {
+    using half8 = _Float16 __attribute__((ext_vector_type(8)));
+    const float qk_scale = kLog2e / 16.0f;
+    const uint32_t kOnes = 0x3c003c00u;
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, p.k[k]), __builtin_bit_cast(half8, qb[k]),
+                                                  s, 0, 0, 0);
+    if (lim < kBlockTokens) {  // the sequence's last page (wave-uniform)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] = (4 * grp + i < lim) ? s[i] : -INFINITY;
+    }
+    const float bm = group4_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+    const float mn = fmaxf(st.m, bm);
+    // Rescale only when some head's max grew (wave-uniform).
+    if (__builtin_amdgcn_ballot_w64(col < G && mn > st.m)) {
+        const float corr = __builtin_amdgcn_exp2f((st.m - mn) * qk_scale);
+        st.l *= corr;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float cg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), g));
+#pragma unroll
+            for (int c = 0; c < 4; ++c) st.acc[g][c] *= cg;
+        }
+        st.m = mn;
+    }
+    const float off = -st.m * qk_scale;
+    const uint32_t pk0 = pack_h2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[0], qk_scale, off)),
+                                 __builtin_amdgcn_exp2f(__builtin_fmaf(s[1], qk_scale, off)));
+    const uint32_t pk1 = pack_h2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2], qk_scale, off)),
+                                 __builtin_amdgcn_exp2f(__builtin_fmaf(s[3], qk_scale, off)));
+    st.l = dot2(pk1, kOnes, dot2(pk0, kOnes, st.l));  // l sums the fp16 probabilities PV uses
+    // Rows 4grp, 4grp+1 are pair 2grp; rows 4grp+2, 4grp+3 pair 2grp+1.  The
+    // wave's LDS operations run in order, so the previous page's reads are
+    // done before these writes land.
+    if (col < 8) {
+        pbuf[(2 * grp) * 8 + col] = pk0;
+        pbuf[(2 * grp + 1) * 8 + col] = pk1;
+    }
+#pragma unroll
+    for (int t = 0; t < kBlockTokens / 2; ++t) {
+        uint32_t pp[8];
+        *reinterpret_cast<uint4 *>(pp) = reinterpret_cast<const uint4 *>(pbuf)[2 * t];
+        if (G > 4) *reinterpret_cast<uint4 *>(pp + 4) = reinterpret_cast<const uint4 *>(pbuf)[2 * t + 1];
+        const uint2 va = p.v[2 * t];
+        const uint2 vb = p.v[2 * t + 1];
+        const uint32_t v0 = (va.x & 0xffffu) | (vb.x << 16);
+        const uint32_t v1 = (va.x >> 16) | (vb.x & 0xffff0000u);
+        const uint32_t v2 = (va.y & 0xffffu) | (vb.y << 16);
+        const uint32_t v3 = (va.y >> 16) | (vb.y & 0xffff0000u);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            st.acc[g][0] = dot2(pp[g], v0, st.acc[g][0]);
+            st.acc[g][1] = dot2(pp[g], v1, st.acc[g][1]);
+            st.acc[g][2] = dot2(pp[g], v2, st.acc[g][2]);
+            st.acc[g][3] = dot2(pp[g], v3, st.acc[g][3]);
+        }
+    }
+}
+
+template <int G>
+__global__ __launch_bounds__(64 * kMfmaWaves) void decode_mfma_kernel(DecodeArgs a) {
+    // Query rows of the range's first kQSlots sequences, per wave (its kv
+    // head); later ones are reloaded kQSlots at a time.
+    constexpr int kQSlots = 4;
+    __shared__ uint4 q_lds[kMfmaWaves * kQSlots * G * 32];
+    __shared__ uint32_t p_lds[kMfmaWaves * 64];
+    __shared__ uint64_t tl_t[2];
+    if (a.timeline && threadIdx.x == 0) tl_t[0] = __builtin_amdgcn_s_memrealtime();
+
+    const int w = blockIdx.x;
+    int P, W;
+    stream_k_shape(a, P, W);
+    if (w >= W) return;
+    const int p_begin = wg_start(w, P, W);
+    const int p_end = wg_start(w + 1, P, W);
+    if (p_begin >= p_end) return;
+    const int hkv = a.num_kv_heads;
+    const int nh = a.num_heads;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = __builtin_amdgcn_readfirstlane(blockIdx.y * (blockDim.x >> 6) + wave);
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int row_bytes = hkv * kHeadDim * 2;
+    const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
+    const uint32_t koff = col * row_bytes + 128 * grp;
+    const uint32_t voff = 8 * lane;
+
+    int b0, b1;
+    if (a.pre_seq) {
+        b0 = 0;
+        b1 = 0;
+        for (int c0 = 0; c0 < a.n_seqs; c0 += 64) {
+            const int i = c0 + lane;
+            const int end = i < a.n_seqs ? a.pre_seq[i + 1] : INT32_MAX;
+            const uint64_t m0 = __ballot(end <= p_begin);
+            const uint64_t m1 = __ballot(end <= p_end - 1);
+            b0 += __popcll(m0);
+            b1 += __popcll(m1);
+            if (m1 != ~0ull) break;
+        }
+    } else {
+        const int npg_c = (a.ctx_len_const + 15) >> 4;
+        b0 = p_begin / npg_c;
+        b1 = (p_end - 1) / npg_c;
+    }
+    b0 = __builtin_amdgcn_readfirstlane(b0);
+    b1 = __builtin_amdgcn_readfirstlane(b1);
+    SeqWindow win;
+    load_window(win, a, b0, lane);
+
+    // This wave's query rows of sequences b .. b+kQSlots-1 (up to b1) into its
+    // own slots; q_hi is the last sequence loaded.  Only this wave reads them.
+    uint4 *q_head = q_lds + wave * kQSlots * G * 32;
+    int q_hi = 0;
+    auto load_q = [&](int b) {
+        q_hi = b + kQSlots - 1;
+        const int n = min(kQSlots, b1 - b + 1);
+        for (int k = 0; k < n; ++k) {
+            const uint16_t *qb =
+                a.q + (static_cast<size_t>(b + k) * nh + static_cast<size_t>(h) * G) * kHeadDim;
+            const int slot = (b + k - b0) % kQSlots;
+#pragma unroll
+            for (int i = lane; i < G * 32; i += 64) q_head[slot * G * 32 + i] = ld16(qb + 8 * i);
+        }
+    };
+    uint4 qb[8];
+    auto fill_q = [&](int b) {
+        const uint4 *qs = q_head + ((b - b0) % kQSlots) * G * 32;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qb[k] = col < G ? qs[col * 32 + 8 * grp + k] : make_uint4(0, 0, 0, 0);
+    };
+    load_q(b0);
+    fill_q(b0);
+
+    const char *kpool = reinterpret_cast<const char *>(a.k_pool) + h * kHeadDim * 2;
+    const char *vpool = reinterpret_cast<const char *>(a.v_pool) + h * kHeadDim * 2;
+    auto page_id = [&](const Cursor &c) -> int {
+        return a.table ? ld_uniform(a.table + static_cast<size_t>(c.sid) * a.table_stride + c.pg) : c.pg;
+    };
+    auto page_ofs = [&](const Cursor &c, int id) -> size_t {
+        const size_t seq = a.table ? 0 : static_cast<size_t>(c.b) * a.seq_stride * 2;
+        return seq + static_cast<size_t>(id) * page_bytes;
+    };
+    auto lim_of = [](const Cursor &c) { return min(kBlockTokens, c.ctx - c.pg * kBlockTokens); };
+    auto next = [&](Cursor c) -> Cursor {
+        if (!c.ok) return c;
+        if (c.base + c.pg + 1 >= p_end) {
+            c.ok = false;
+            return c;
+        }
+        if (c.pg + 1 < c.npg) {
+            ++c.pg;
+            return c;
+        }
+        int b = c.b;
+        do {
+            ++b;
+            if (b - win.b0 >= 64) load_window(win, a, b, lane);
+            c = seq_cursor(win, b);
+        } while (c.npg == 0);
+        return c;
+    };
+
+    MfmaState<G> st;
+    reset(st);
+    // End of sequence c.b in this range: the wave writes its head's output
+    // (whole sequence) or this range's partial, then loads the next rows.
+    auto finish = [&](const Cursor &c, int b_next) {
+        const float qk_scale = kLog2e / 16.0f;
+        const float lt = group4_sum(st.l);  // the four lane groups hold disjoint rows
+        const bool whole = c.base >= p_begin && c.base + c.npg <= p_end;
+        const int slot = 2 * w + (c.b == b0 ? 0 : 1);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, st.m), g));
+            const float lg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lt), g));
+            if (whole) {
+                const float inv = 1.0f / lg;
+                *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(c.b) * nh + h * G + g) * kHeadDim +
+                                           4 * lane) =
+                    out_fp16x4(st.acc[g][0] * inv, st.acc[g][1] * inv, st.acc[g][2] * inv, st.acc[g][3] * inv,
+                               gate_of(a, c.b, h * G + g, lane));
+            } else {
+                const size_t u = (static_cast<size_t>(slot) * hkv + h) * G + g;
+                *reinterpret_cast<float4 *>(a.ws_acc + u * kHeadDim + 4 * lane) =
+                    make_float4(st.acc[g][0], st.acc[g][1], st.acc[g][2], st.acc[g][3]);
+                if (lane == 0) {
+                    a.ws_ml[u * 2] = mg * qk_scale;  // log2 units
+                    a.ws_ml[u * 2 + 1] = lg;
+                }
+            }
+        }
+        if (b_next > q_hi) load_q(b_next);
+        reset(st);
+    };
+
+    // Two page buffers: while one is folded in, the next page is in flight.
+    Page A, B;
+    Cursor c0 = seq_cursor(win, b0);
+    c0.pg = p_begin - c0.base;
+    Cursor cq[2];
+    cq[0] = c0;
+    cq[1] = next(c0);
+    int id_last = 0;
+    {
+        const int id = page_id(cq[0]);
+        load_page(A, kpool + page_ofs(cq[0], id), vpool + page_ofs(cq[0], id), lim_of(cq[0]), true, koff, voff,
+                  row_bytes);
+        id_last = cq[1].ok ? page_id(cq[1]) : id;
+    }
+    if (a.timeline && threadIdx.x == 0) tl_t[1] = __builtin_amdgcn_s_memrealtime();
+    uint32_t *pbuf = p_lds + 64 * wave;
+    auto step = [&](Page &cr, Page &nr) -> bool {
+        const Cursor cl = cq[1];
+        const Cursor cn = next(cl);
+        const int id_n = cn.ok ? page_id(cn) : id_last;
+        load_page(nr, kpool + page_ofs(cl, id_last), vpool + page_ofs(cl, id_last), lim_of(cl), cl.ok, koff, voff,
+                  row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+        const Cursor cur = cq[0];
+        compute_page<G>(st, cr, qb, lane, lim_of(cur), pbuf);
+        if (!cq[1].ok || cq[1].b != cur.b) {
+            finish(cur, cq[1].ok ? cq[1].b : 0);
+            if (cq[1].ok) fill_q(cq[1].b);
+        }
+        cq[0] = cq[1];
+        cq[1] = cn;
+        id_last = id_n;
+        return cq[0].ok;
+    };
+    while (step(A, B) && step(B, A)) {
+    }
+    if (a.timeline && lane == 0) {
+        // decode_kernel's record layout (eight per workgroup); the records of
+        // waves this workgroup does not have are zero.
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        uint64_t *rec = a.timeline + ((static_cast<size_t>(w) * gridDim.y + blockIdx.y) * 8 + wave) * kTimelineWords;
+        rec[0] = tl_t[0];
+        rec[1] = tl_t[1];
+        rec[2] = __builtin_amdgcn_s_memrealtime();
+        rec[3] = (static_cast<uint64_t>(xcc & 0xf) << 32) | static_cast<uint32_t>(p_end - p_begin);
+        for (int v = wave + (blockDim.x >> 6); v < 8; v += blockDim.x >> 6)
+            for (int i = 0; i < kTimelineWords; ++i)
+                a.timeline[((static_cast<size_t>(w) * gridDim.y + blockIdx.y) * 8 + v) * kTimelineWords + i] = 0;
+    }
+}
+
 // Merge the partials of one (sequence, kv head, query head of the group)
 // whose pages were cut across workgroups: 64 lanes x 4 dims per wave.  A
 // separate launch (stream order makes the partials visible), so no
@@ -916,6 +1236,16 @@ hipError_t launch_whole(const DecodeArgs &a, hipStream_t s) {
 
 template <int G>
 hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
+    if (a.mfma) {
+        int hpw = a.num_kv_heads <= kMfmaWaves ? a.num_kv_heads : kMfmaWaves;
+        while (a.num_kv_heads % hpw) --hpw;
+        hipLaunchKernelGGL(decode_mfma_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(64 * hpw), 0, s, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * kCombineWaves), 0, s,
+                           a);
+        return hipGetLastError();
+    }
     // Kv heads per workgroup (two waves each): all of them up to
     // kDecodeHeadsPerWg (two waves per SIMD at 512 threads), else the largest
     // divisor of Hkv that is at most that.

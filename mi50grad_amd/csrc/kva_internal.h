@@ -160,6 +160,9 @@ struct DecodeArgs {
     // new token joins the attention from registers, not from the cache.
     int32_t fused;
     AppendArgs app;
+    // 1: stream-K with QK on the matrix cores (decode_mfma_kernel, one wave
+    // per kv head); the same split, partials and combine.
+    int32_t mfma;
 };
 constexpr int kTimelineWords = 4;
 constexpr int kWholeWaves = 8;  // waves per whole-sequence decode workgroup

@@ -1,8 +1,9 @@
 """GPU: the decode timeline (kva_timeline_enable / kva_timeline_read).
 
 The records must describe the launch that ran (one per wave of every
-workgroup, entry <= first K/V issue <= walk end, an XCD id below 8, page
-counts that add up to the step's pages; for the whole-sequence form, one
+workgroup, zero for waves a workgroup does not have, entry <= first K/V
+issue <= walk end, an XCD id below 8, page counts that add up to the step's
+pages; for the whole-sequence form, one
 workgroup per sequence and kv head with that sequence's pages) and recording
 must not change the decode's output (bit-equal to the same decode with the
 timeline off).  Refused before it is enabled.
@@ -43,11 +44,14 @@ def test_timeline_records_the_launch_and_leaves_the_output_alone():
     assert rec.shape == (n_wg, 1, 8, 4)
     assert np.array_equal(out_on.numpy().view(np.uint16), out_off.numpy().view(np.uint16))
     ent, first, end, meta = (rec[..., i] for i in range(4))
-    assert (ent > 0).all() and (ent <= first).all() and (first <= end).all()
-    assert (((meta >> 32) & 0xF) < 8).all()
+    ran = ent > 0  # waves a workgroup does not have leave zero records
+    assert ran[:, :, 0].all() and (rec[~ran] == 0).all()
+    assert (ent[ran] <= first[ran]).all() and (first[ran] <= end[ran]).all()
+    assert (((meta[ran] >> 32) & 0xF) < 8).all()
     pages = (meta & 0xFFFFFFFF)[:, 0, 0]
     assert int(pages.sum()) == sum(npg) and (pages > 0).all()
-    assert (meta[:, :, :1] == meta).all()  # every wave of a workgroup reports the same range
+    same = np.broadcast_to(meta[:, :, :1], meta.shape)
+    assert (meta[ran] == same[ran]).all()  # every wave of a workgroup reports the same range
     cache.timeline_enable(False)
     with pytest.raises(_lib.KvaError, match="not enabled"):
         cache.timeline()
