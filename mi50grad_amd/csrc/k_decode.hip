@@ -1,27 +1,33 @@
-// Split-K GQA flash-decode over the paged FP16 cache (gfx950, VALU path).
+// GQA flash-decode over the paged FP16 cache (gfx950).
 //
 // Semantics: flash_attn_256_decode (flash_attn_256_tuned.hip:198-350) —
 // out = softmax(q K^T / sqrt(256)) V per query head, kv head = h*Hkv/H
 // (:222) — generalised to a batch of sequences with ragged lengths read
-// through a block table, and to any number of KV splits.
+// through a block table, and to any split of the keys.  The G = H/Hkv query
+// heads of a kv head share every K/V byte a wave loads (the reference
+// re-read each kv head G times, once per query head).
 //
-// Work split: stream-K over pages (see decode_kernel).  A workgroup holds two
-// waves per kv head; both walk the same pages, wave k taking tokens
-// 8k..8k+7 of every 16-token page, and merge through LDS when a sequence
-// ends.  The G = H/Hkv query heads of a KV head share every K/V byte its
-// waves load (the reference re-read each KV head G times, once per query
-// head).  Two waves per SIMD hide each other's load waits and issue turns.
+// Three launches:
+//   decode_mfma_kernel + combine_kernel: stream-K over pages for long steps.
+//       The pages of every sequence are laid end to end and workgroup w
+//       takes [w*P/W, (w+1)*P/W), equal shares whatever the ragged lengths;
+//       one wave per kv head walks every page of the share, QK on the
+//       matrix cores, PV on v_dot2_f32_f16.  A sequence the share covers
+//       whole is written out directly; a cut one leaves a partial (m, l,
+//       acc) per head for combine_kernel.
+//   whole_kernel: steps of short sequences (no combine): a workgroup walks
+//       one sequence for one kv head and a group of its query heads, eight
+//       waves on half pages with QK and PV on v_dot2_f32_f16 (below),
+//       merged through LDS; optionally with the step's append fused in.
 //
-// Per page half, per wave (lane = 16*r + j):
-//   loads: a ring of three register buffers; while one half page is folded
-//       in, the next two pages' halves (16 KB per wave) are in flight, across
-//       sequence boundaries too.  Buffer loads through a per-page resource: its range
-//       check zero-fills rows past a sequence's end and turns a prefetch past
-//       the range into a no-op that still counts;
+// The whole-sequence form's half page, per wave (lane = 16*r + j):
+//   loads: a ring of register buffers; buffer loads through a per-page
+//       resource whose range check zero-fills rows past a sequence's end
+//       and turns a prefetch past the range into a no-op that still counts;
 //   QK: the 16 lanes of row r hold tokens 8k+r and 8k+r+4, 16 dims each
-//       (16-byte pieces j and j+16 of the 512-byte row: each load is 256
-//       contiguous bytes per token), dot with the G query rows (held in
-//       registers) via v_dot2_f32_f16; a 16-lane DPP sum finishes each score;
+//       (16-byte pieces j and j+16 of the 512-byte row), dot with the G query
+//       rows (held in registers) via v_dot2_f32_f16; a 16-lane DPP sum
+//       finishes each score;
 //   softmax: log2 domain; max over the four rows with row-broadcast DPP and
 //       one v_readlane (no LDS round trips); v_exp_f32; probabilities
 //       rounded to fp16 pairs;
@@ -289,284 +295,11 @@ __device__ __forceinline__ Cursor seq_cursor(const SeqWindow &win, int b) {
     return c;
 }
 
-// Stream-K decode: the pages of every sequence are laid end to end and
-// workgroup w takes pages [wg_start(w), wg_start(w+1)) — equal shares,
-// whatever the ragged lengths.  Waves 2h and 2h+1 of the workgroup serve kv
-// head h, so the workgroup reads the Hkv head slices of the same token rows
-// together (whole 2 KB rows, whole 32 KB pages).  One pipeline walks the
-// whole range, so the first page of the next sequence is in flight while the
-// last of the current one is folded in.  At a sequence's end the two waves of
-// each head merge through LDS; a sequence the range covers whole is written
-// out directly, a sequence cut by a range boundary leaves a partial (m, l,
-// acc) per head in slot 2w (the range's first sequence) or 2w+1 (its last)
-// for combine_kernel.
-template <int G>
-__global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeArgs a) {
-    // Query rows of the range's first kQSlots sequences per head in LDS (both
-    // waves of the head read them); later ones are reloaded kQSlots at a time.
-    constexpr int kQSlots = (24 / G) > 2 ? (24 / G) : 2;
-    __shared__ uint4 q_lds[kDecodeHeadsPerWg * kQSlots * G * 32];
-    // Per-wave broadcast buffer for PV's probability pairs.
-    __shared__ uint32_t p_lds[2 * kDecodeHeadsPerWg * 32];
-    // Wave 2h+1's state for wave 2h to merge at a sequence end.
-    __shared__ float4 mrg_acc[kDecodeHeadsPerWg * G * 64];
-    __shared__ float mrg_ml[kDecodeHeadsPerWg * G * 2];
-    // Timeline (a.timeline set): entry and first-issue times, kept in LDS so
-    // they hold no registers across the walk.
-    __shared__ uint64_t tl_t[2];
-    if (a.timeline && threadIdx.x == 0) tl_t[0] = __builtin_amdgcn_s_memrealtime();
-
-    const int w = blockIdx.x;
-    int P, W;
-    stream_k_shape(a, P, W);
-    if (w >= W) return;  // a recorded launch's grid is the cap
-    const int p_begin = wg_start(w, P, W);
-    const int p_end = wg_start(w + 1, P, W);
-    if (p_begin >= p_end) return;  // uniform over the workgroup
-    const int hkv = a.num_kv_heads;
-    const int nh = a.num_heads;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int hl = wave >> 1;  // head within the workgroup
-    const int half = wave & 1;  // tokens 8*half .. 8*half+7 of each page
-    // This wave's kv head: grid.y splits the heads when more than fit one
-    // workgroup.
-    const int h = __builtin_amdgcn_readfirstlane(blockIdx.y * (blockDim.x >> 7) + hl);
-    const int lane = threadIdx.x & 63;
-    const int r = lane >> 4;
-    const int j = lane & 15;
-    const int row_bytes = hkv * kHeadDim * 2;
-    const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
-    const uint32_t koff = (kHalf * half + r) * row_bytes + 16 * j;
-    const uint32_t voff = kHalf * half * row_bytes + 8 * lane;
-
-    // Sequences holding the first and the last page of the range: the number
-    // of sequences that end at or before the page (a ballot per 64).
-    int b0, b1;
-    if (a.pre_seq) {
-        b0 = 0;
-        b1 = 0;
-        for (int c0 = 0; c0 < a.n_seqs; c0 += 64) {
-            const int i = c0 + lane;
-            const int end = i < a.n_seqs ? a.pre_seq[i + 1] : INT32_MAX;
-            const uint64_t m0 = __ballot(end <= p_begin);
-            const uint64_t m1 = __ballot(end <= p_end - 1);
-            b0 += __popcll(m0);
-            b1 += __popcll(m1);
-            if (m1 != ~0ull) break;
-        }
-    } else {
-        const int npg_c = (a.ctx_len_const + 15) >> 4;
-        b0 = p_begin / npg_c;
-        b1 = (p_end - 1) / npg_c;
-    }
-    b0 = __builtin_amdgcn_readfirstlane(b0);
-    b1 = __builtin_amdgcn_readfirstlane(b1);
-    SeqWindow win;
-    load_window(win, a, b0, lane);
-
-    // Query rows of sequences b .. b+kQSlots-1 (up to b1) into this head's
-    // slots, half by each of its two waves; q_hi is the last sequence loaded.
-    // Callers pass a barrier before the rows are read.
-    uint4 *q_head = q_lds + hl * kQSlots * G * 32;
-    int q_hi = 0;
-    auto load_q = [&](int b) {
-        q_hi = b + kQSlots - 1;
-        const int n = min(kQSlots, b1 - b + 1);
-        for (int k = 0; k < n; ++k) {
-            const uint16_t *qb =
-                a.q + (static_cast<size_t>(b + k) * nh + static_cast<size_t>(h) * G) * kHeadDim;
-            const int slot = (b + k - b0) % kQSlots;
-#pragma unroll
-            for (int i = lane + 64 * half; i < G * 32; i += 128) q_head[slot * G * 32 + i] = ld16(qb + 8 * i);
-        }
-    };
-    // The current sequence's query pieces j and j+16, in registers; refilled
-    // from LDS (no memory round trip) when the walk enters a new sequence.
-    uint4 qv[G][2];
-    auto fill_q = [&](int b) {
-        const uint4 *qs = q_head + ((b - b0) % kQSlots) * G * 32;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            qv[g][0] = qs[g * 32 + j];
-            qv[g][1] = qs[g * 32 + 16 + j];
-        }
-    };
-    load_q(b0);
-    __syncthreads();
-    fill_q(b0);
-
-    const char *kpool = reinterpret_cast<const char *>(a.k_pool) + h * kHeadDim * 2;
-    const char *vpool = reinterpret_cast<const char *>(a.v_pool) + h * kHeadDim * 2;
-    auto page_id = [&](const Cursor &c) -> int {
-        return a.table ? ld_uniform(a.table + static_cast<size_t>(c.sid) * a.table_stride + c.pg) : c.pg;
-    };
-    auto page_ofs = [&](const Cursor &c, int id) -> size_t {
-        const size_t seq = a.table ? 0 : static_cast<size_t>(c.b) * a.seq_stride * 2;
-        return seq + static_cast<size_t>(id) * page_bytes;
-    };
-    auto lim_of = [](const Cursor &c) { return min(kBlockTokens, c.ctx - c.pg * kBlockTokens); };
-    // The page after c in the range (skipping empty sequences).
-    auto next = [&](Cursor c) -> Cursor {
-        if (!c.ok) return c;
-        if (c.base + c.pg + 1 >= p_end) {
-            c.ok = false;
-            return c;
-        }
-        if (c.pg + 1 < c.npg) {
-            ++c.pg;
-            return c;
-        }
-        int b = c.b;
-        do {
-            ++b;
-            if (b - win.b0 >= 64) load_window(win, a, b, lane);
-            c = seq_cursor(win, b);
-        } while (c.npg == 0);
-        return c;
-    };
-
-    WaveState<G> st;
-    reset(st);
-    // End of sequence c.b in this range: wave 2h+1 hands its state to wave
-    // 2h through LDS, which merges and writes the output (whole sequence) or
-    // this range's partial.  Every wave of the workgroup reaches the two
-    // barriers together: they all walk the same pages.
-    auto finish = [&](const Cursor &c, int b_next) {
-        const float qk_scale = kLog2e / 16.0f;
-        float lt[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {  // the four rows hold disjoint tokens
-            lt[g] = st.l[g];
-            lt[g] += __shfl_xor(lt[g], 16);
-            lt[g] += __shfl_xor(lt[g], 32);
-        }
-        if (half == 1) {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                mrg_acc[(hl * G + g) * 64 + lane] = make_float4(st.acc[g][0], st.acc[g][1], st.acc[g][2], st.acc[g][3]);
-                if (lane == 0) {
-                    mrg_ml[(hl * G + g) * 2] = st.m[g];
-                    mrg_ml[(hl * G + g) * 2 + 1] = lt[g];
-                }
-            }
-        }
-        if (b_next > q_hi) load_q(b_next);
-        __syncthreads();
-        if (half == 0) {
-            const bool whole = c.base >= p_begin && c.base + c.npg <= p_end;
-            const int slot = 2 * w + (c.b == b0 ? 0 : 1);
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                // Wave 0 of the pair always saw token 0 of every page: its m is finite.
-                const float m1 = mrg_ml[(hl * G + g) * 2];
-                const float l1 = mrg_ml[(hl * G + g) * 2 + 1];
-                const float4 a1 = mrg_acc[(hl * G + g) * 64 + lane];
-                const float mm = fmaxf(st.m[g], m1);
-                const float c0 = __builtin_amdgcn_exp2f((st.m[g] - mm) * qk_scale);
-                const float c1 = __builtin_amdgcn_exp2f((m1 - mm) * qk_scale);
-                const float l = lt[g] * c0 + l1 * c1;
-                const float o0 = st.acc[g][0] * c0 + a1.x * c1;
-                const float o1 = st.acc[g][1] * c0 + a1.y * c1;
-                const float o2 = st.acc[g][2] * c0 + a1.z * c1;
-                const float o3 = st.acc[g][3] * c0 + a1.w * c1;
-                if (whole) {
-                    const float inv = 1.0f / l;
-                    *reinterpret_cast<uint2 *>(a.out + (static_cast<size_t>(c.b) * nh + h * G + g) * kHeadDim +
-                                               4 * lane) =
-                        out_fp16x4(o0 * inv, o1 * inv, o2 * inv, o3 * inv, gate_of(a, c.b, h * G + g, lane));
-                } else {
-                    const size_t u = (static_cast<size_t>(slot) * hkv + h) * G + g;
-                    *reinterpret_cast<float4 *>(a.ws_acc + u * kHeadDim + 4 * lane) = make_float4(o0, o1, o2, o3);
-                    if (lane == 0) {
-                        a.ws_ml[u * 2] = mm * qk_scale;  // log2 units
-                        a.ws_ml[u * 2 + 1] = l;
-                    }
-                }
-            }
-        }
-        __syncthreads();
-        reset(st);
-    };
-
-    // Half-page buffers in a ring of kStages: while one is folded in, the
-    // next pages' halves are in flight (with three, about 128 KB per CU,
-    // what HBM's loaded latency needs; G = 8 keeps two to stay within 256
-    // VGPRs).  Every step issues the same loads (a prefetch past the range
-    // goes through an empty resource), so the compiler's load counters stay
-    // exact and waiting for one buffer never drains the others.
-    constexpr int kStages = G <= 6 ? 3 : 2;
-    HalfPage A, B, C;
-    Cursor c0 = seq_cursor(win, b0);  // window lane 0 is b0
-    c0.pg = p_begin - c0.base;
-    // cq[0] is folded in this step, cq[1..kStages-2] are in flight, and
-    // cq[kStages-1] (with id_last) is issued this step.
-    Cursor cq[kStages];
-    cq[0] = c0;
-    for (int i = 1; i < kStages; ++i) cq[i] = next(cq[i - 1]);
-    int id_last = 0;
-    {
-        int id = page_id(cq[0]);
-        load_half(A, kpool + page_ofs(cq[0], id), vpool + page_ofs(cq[0], id), lim_of(cq[0]), true, koff, voff,
-                  row_bytes);
-        if (kStages == 3) {
-            id = cq[1].ok ? page_id(cq[1]) : id;
-            load_half(B, kpool + page_ofs(cq[1], id), vpool + page_ofs(cq[1], id), lim_of(cq[1]), cq[1].ok, koff,
-                      voff, row_bytes);
-        }
-        id_last = cq[kStages - 1].ok ? page_id(cq[kStages - 1]) : id;
-    }
-    if (a.timeline && threadIdx.x == 0) tl_t[1] = __builtin_amdgcn_s_memrealtime();
-    // One step: issue cq[last] into `nr`, fold cq[0] (in `cr`) in, finish the
-    // sequence when the next page belongs to another one.
-    auto step = [&](HalfPage &cr, HalfPage &nr) -> bool {
-        const Cursor cl = cq[kStages - 1];
-        const Cursor cn = next(cl);
-        const int id_n = cn.ok ? page_id(cn) : id_last;
-        load_half(nr, kpool + page_ofs(cl, id_last), vpool + page_ofs(cl, id_last), lim_of(cl), cl.ok, koff,
-                  voff, row_bytes);
-        __builtin_amdgcn_sched_barrier(0);
-        const Cursor cur = cq[0];
-        const int lim = lim_of(cur) - kHalf * half;  // valid tokens of this wave's half
-        if (lim > 0) {
-            compute_half<G>(st, cr, qv, r, j, min(lim, kHalf), p_lds + 32 * wave);
-        } else {
-            consume(cr);
-        }
-        if (!cq[1].ok || cq[1].b != cur.b) {
-            finish(cur, cq[1].ok ? cq[1].b : 0);
-            if (cq[1].ok) fill_q(cq[1].b);
-        }
-#pragma unroll
-        for (int i = 0; i + 1 < kStages; ++i) cq[i] = cq[i + 1];
-        cq[kStages - 1] = cn;
-        id_last = id_n;
-        return cq[0].ok;
-    };
-    if constexpr (kStages == 3) {
-        while (step(A, C) && step(B, A) && step(C, B)) {
-        }
-    } else {
-        while (step(A, B) && step(B, A)) {
-        }
-    }
-    if (a.timeline && lane == 0) {
-        // Per wave: entry, first K/V issue, end of its walk (100 MHz
-        // s_memrealtime ticks), then the XCD (high word) and the range's pages.
-        uint32_t xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-        uint64_t *rec = a.timeline + ((static_cast<size_t>(w) * gridDim.y + blockIdx.y) * 8 + wave) * kTimelineWords;
-        rec[0] = tl_t[0];
-        rec[1] = tl_t[1];
-        rec[2] = __builtin_amdgcn_s_memrealtime();
-        rec[3] = (static_cast<uint64_t>(xcc & 0xf) << 32) | static_cast<uint32_t>(p_end - p_begin);
-    }
-}
-
 // ---- Stream-K decode with QK on the matrix cores ----
 //
-// The same page split, partial slots and combine as decode_kernel, with one
-// wave per kv head walking every page of the workgroup's range (16 token
-// rows a step) and no cross-wave merge.
+// One wave per kv head walks every page of the workgroup's share (16 token
+// rows a step), so no waves merge inside the workgroup; at a sequence end the
+// wave writes its head's output or the share's partial itself.
 //   QK: S^T = K Q^T on v_mfma_f32_16x16x32_f16, the page's 16 rows as the A
 //       operand and the G query rows as columns 0..G-1 of B (the others
 //       zero).  The k order inside the product is free as long as A and B
@@ -576,7 +309,13 @@ __global__ __launch_bounds__(128 * kDecodeHeadsPerWg) void decode_kernel(DecodeA
 //       the column max over the four lane groups by permlane swaps.
 //   PV: the fp16 probability pairs go through 64 dwords of LDS per wave
 //       ([token pair][head]) to every lane, which folds token pairs with
-//       v_dot2_f32_f16 into dims 4l..4l+3 of every head, as decode_kernel.
+//       v_dot2_f32_f16 into dims 4l..4l+3 of every head (the whole-sequence
+//       form's PV, over sixteen rows).
+// Measured against the previous stream-K kernel (eight waves on half pages,
+// QK and PV on the VALU), config 3 went from 130.8 to 120.0 us per call and
+// ctx 8192 from 203 to 188: the VALU work per page of a kv head roughly
+// halves, and one workgroup of four waves per CU (one wave per SIMD) beats
+// two (126 us).
 constexpr int kMfmaWaves = kDecodeHeadsPerWg;  // waves (kv heads) per workgroup, at most
 
 struct Page {
@@ -867,8 +606,10 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void decode_mfma_kernel(DecodeArgs
     while (step(A, B) && step(B, A)) {
     }
     if (a.timeline && lane == 0) {
-        // decode_kernel's record layout (eight per workgroup); the records of
-        // waves this workgroup does not have are zero.
+        // Per wave: entry, first K/V issue, end of its walk (100 MHz
+        // s_memrealtime ticks), then the XCD (high word) and the share's
+        // pages; eight records per workgroup row, zero for the waves this
+        // workgroup does not have.
         uint32_t xcc;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
         uint64_t *rec = a.timeline + ((static_cast<size_t>(w) * gridDim.y + blockIdx.y) * 8 + wave) * kTimelineWords;
@@ -1149,8 +890,8 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
         }
     }
     if (a.timeline && lane == 0) {
-        // As decode_kernel's records, one row per workgroup of unit u's
-        // group z: [n_units * n_grp][1][8 waves].
+        // As decode_mfma_kernel's records, one row per workgroup of unit
+        // u's group z: [n_units * n_grp][1][8 waves].
         uint32_t xcc;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
         uint64_t *rec =
@@ -1236,24 +977,14 @@ hipError_t launch_whole(const DecodeArgs &a, hipStream_t s) {
 
 template <int G>
 hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
-    if (a.mfma) {
-        int hpw = a.num_kv_heads <= kMfmaWaves ? a.num_kv_heads : kMfmaWaves;
-        while (a.num_kv_heads % hpw) --hpw;
-        hipLaunchKernelGGL(decode_mfma_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(64 * hpw), 0, s, a);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * kCombineWaves), 0, s,
-                           a);
-        return hipGetLastError();
-    }
-    // Kv heads per workgroup (two waves each): all of them up to
-    // kDecodeHeadsPerWg (two waves per SIMD at 512 threads), else the largest
-    // divisor of Hkv that is at most that.
-    int hpw = a.num_kv_heads <= kDecodeHeadsPerWg ? a.num_kv_heads : kDecodeHeadsPerWg;
+    // Kv heads (one wave each) per workgroup: all of them up to kMfmaWaves,
+    // else the largest divisor of Hkv that is at most that; grid rows split
+    // the rest.
+    int hpw = a.num_kv_heads <= kMfmaWaves ? a.num_kv_heads : kMfmaWaves;
     while (a.num_kv_heads % hpw) --hpw;
-    hipLaunchKernelGGL(decode_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(128 * hpw), 0, s, a);
+    hipLaunchKernelGGL(decode_mfma_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(64 * hpw), 0, s, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !a.ws_acc) return e;
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * kCombineWaves), 0, s, a);
     return hipGetLastError();
 }

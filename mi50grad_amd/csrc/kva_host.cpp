@@ -53,10 +53,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 constexpr int kStageSlots = 4;
 constexpr int kDecodeWgPerCu = 1;   // stream-K decode workgroups per CU
-// Stream-K decode with QK on the matrix cores (decode_mfma_kernel): config 3
-// 130.8 -> 120.0 us per call, ctx 8192 203.2 -> 187.7 us against the VALU
-// kernel (decode_kernel), which stays for comparison.
-constexpr bool kDecodeMfma = true;
+
 constexpr int kMinPagesPerWg = 1;   // a short sequence still spreads over several CUs
 // A decode step (automatic split) whose longest sequence has at most this
 // many rows runs the whole-sequence form: one workgroup per sequence and kv
@@ -1095,7 +1092,6 @@ static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_
     a.ws_acc = c->d_ws_acc;
     a.ws_ml = c->d_ws_ml;
     a.timeline = c->d_timeline;
-    a.mfma = kDecodeMfma ? 1 : 0;
     c->last_nwg = a.n_wg;
     c->last_split = static_cast<int32_t>((pages * kva::kBlockTokens + a.n_wg - 1) / a.n_wg);
 }
@@ -1633,7 +1629,6 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
                                   (pages + kMinPagesPerWg - 1) / kMinPagesPerWg, fit})));
         a.ws_acc = static_cast<float *>(scratch);
         a.ws_ml = a.ws_acc + static_cast<size_t>(2) * a.n_wg * num_heads * kva::kHeadDim;
-        a.mfma = kDecodeMfma ? 1 : 0;
     } else {
         set_stream_k(ws, a, pages, num_heads);
     }

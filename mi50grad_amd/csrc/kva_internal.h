@@ -12,7 +12,7 @@ namespace kva {
 
 constexpr int kHeadDim = 256;     // the only head_dim the paged kernels take
 constexpr int kBlockTokens = 16;  // tokens per page
-constexpr int kDecodeHeadsPerWg = 4;  // kv heads per decode workgroup (two waves each), at most
+constexpr int kDecodeHeadsPerWg = 4;  // kv heads per stream-K decode workgroup (one wave each), at most
 constexpr int kSplitQuantum = 16; // decode split sizes are whole pages
 
 // Fused QK-RMSNorm + RoPE + K/V append over all new tokens of a step.
@@ -137,8 +137,7 @@ struct DecodeArgs {
     int32_t dyn;
     int32_t split_tokens;     // 0 = one workgroup per CU up to the cap
     int32_t min_pages;
-    float *ws_acc;            // [2*n_wg][Hkv][G][256] partial slots; null = every
-                              // sequence is whole in one workgroup (no combine)
+    float *ws_acc;            // [2*n_wg][Hkv][G][256] partial slots
     float *ws_ml;             // [2*n_wg][Hkv][G][2]
     uint16_t *out;            // [n_seqs][H][256]
     // Output gate (null = none): out = fp16(fp16(attn) * sigmoid(gate)), the
@@ -160,9 +159,6 @@ struct DecodeArgs {
     // new token joins the attention from registers, not from the cache.
     int32_t fused;
     AppendArgs app;
-    // 1: stream-K with QK on the matrix cores (decode_mfma_kernel, one wave
-    // per kv head); the same split, partials and combine.
-    int32_t mfma;
 };
 constexpr int kTimelineWords = 4;
 constexpr int kWholeWaves = 8;  // waves per whole-sequence decode workgroup

@@ -194,10 +194,11 @@ def test_legacy_decode_reference_shapes(device, h, hkv, L):
     assert max_err(out.numpy(), ref) <= TOL
 
 
-@pytest.mark.parametrize("h,hkv", [(24, 4), (32, 4), (24, 8)])
+@pytest.mark.parametrize("h,hkv", [(24, 4), (32, 4), (24, 8), (4, 4), (8, 4), (16, 4), (8, 2)])
 def test_legacy_decode_split_groups(device, h, hkv):
     """Every GQA group width through cut sequences and the combine: a
-    workspace with 128-token splits over a contiguous cache (G = 6, 8, 3)."""
+    workspace with 128-token splits over a contiguous cache (G = 6, 8, 3,
+    1, 2, 4, and 4 on two kv heads)."""
     rng = np.random.default_rng(40 + h + hkv)
     L = 1000
     Q = rng.standard_normal((1, h, D), dtype=np.float32).astype(np.float16)
