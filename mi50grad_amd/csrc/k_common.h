@@ -122,6 +122,14 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// The XCD (accelerator complex die) this wave runs on: CUs of one XCD
+// share its L2.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 0xfu;
+}
+
 // Read-only buffer resource over [base, base + bytes); bytes = 0 makes every
 // access out of range (loads fetch nothing, and still count).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ro_rsrc(const void *base, uint32_t bytes) {

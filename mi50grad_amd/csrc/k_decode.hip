@@ -610,8 +610,7 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void decode_mfma_kernel(DecodeArgs
         // s_memrealtime ticks), then the XCD (high word) and the share's
         // pages; eight records per workgroup row, zero for the waves this
         // workgroup does not have.
-        uint32_t xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        const uint32_t xcc = xcc_id();
         uint64_t *rec = a.timeline + ((static_cast<size_t>(w) * gridDim.y + blockIdx.y) * 8 + wave) * kTimelineWords;
         rec[0] = tl_t[0];
         rec[1] = tl_t[1];
@@ -892,8 +891,7 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     if (a.timeline && lane == 0) {
         // As decode_mfma_kernel's records, one row per workgroup of unit
         // u's group z: [n_units * n_grp][1][8 waves].
-        uint32_t xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        const uint32_t xcc = xcc_id();
         uint64_t *rec =
             a.timeline + ((static_cast<size_t>(u) * n_grp + z) * kWholeWaves + wave) * kTimelineWords;
         rec[0] = tl_t[0];

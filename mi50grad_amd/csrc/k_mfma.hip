@@ -14,18 +14,20 @@
 // row — every head of the group attends to the same K/V — so four waves of
 // 16 x NT rows each (Q = 64*NT/G) leave at most G-1 rows idle (the tree
 // verify's 9 nodes x 6 heads fill 54 of 64 rows).  Work is split stream-K
-// over 32-key blocks: the blocks of all units are laid end to end, head-major
+// over key blocks (64 keys for prefill steps of eight-wave tiles, 32
+// otherwise: mq_keys_for): the blocks of all units are laid end to end, head-major
 // (kv head, sequence, tile), and each workgroup takes an equal share, the
 // shares dealt out XCD by XCD so the tiles of one (sequence, head) run on
 // one XCD and their repeated reads of its keys come from that XCD's L2;
 // units cut by a share boundary leave partials for mq_combine_kernel.
 //
 // K/V blocks travel HBM -> LDS by buffer loads that write LDS directly (no
-// register staging), through a ring of four 32 KB stages: while block i is
-// computed, blocks i+1..i+3 (96 KB) are in flight.  Each wave issues the
-// loads of 8 keys of every block; a wave waits for its own loads of block i
-// (vmcnt) and one workgroup barrier makes all of them visible and frees the
-// stage of block i-1 for block i+3.  Rows are stored with an XOR swizzle of
+// register staging), through a ring of LDS stages: four of 32 keys (while
+// block i is computed, blocks i+1..i+3, 96 KB, are in flight) or two of 64
+// keys (block i+1, 64 KB).  Each wave issues the loads of KEYS/WAVES keys of
+// every block; a wave waits for its own loads of block i (vmcnt) and one
+// workgroup barrier makes all of them visible and frees the stage of block
+// i-1 for the next issue.  Rows are stored with an XOR swizzle of
 // their 16-byte granules so both read patterns below are conflict-free.
 //
 // Per block, wave and 16-row tile t (v_mfma_f32_16x16x32_f16, C layout:
@@ -46,10 +48,11 @@
 namespace kva {
 namespace {
 
-constexpr int kRing = 4;                            // LDS stages
 constexpr int kRowBytes = kHeadDim * 2;             // 512 B: one key of one head
 constexpr int kPairBytes = 2 * kRowBytes + 32;      // two keys, then 32 B of padding
-constexpr int kTileBytes = kMqKeys / 2 * kPairBytes;  // K or V of a block (16.5 KB)
+// LDS stages of the ring for blocks of KEYS keys: 4 x 33 KB or 2 x 66 KB.
+template <int KEYS> constexpr int ring_stages() { return KEYS == 32 ? 4 : 2; }
+template <int KEYS> constexpr int tile_bytes() { return KEYS / 2 * kPairBytes; }  // K or V of a block
 constexpr float kLog2e = 1.4426950408889634f;
 
 
@@ -103,10 +106,11 @@ struct Unit {
 // upre[n_seqs], one head's units), and sequence b holds tiles
 // [upre[b], upre[b+1]).  b is a hint (a sequence at or before the unit's
 // within the same head), so a walk in unit order scans each sequence once.
+template <int KEYS>
 __device__ __forceinline__ Unit load_unit(const MultiQueryArgs &a, int u, int b) {
     Unit x;
     x.u = u;
-    x.ub = ld_uniform(a.mq_pre + u) + kMqUnitCost;  // its first block (positions before: the start cost)
+    x.ub = ld_uniform(a.mq_pre + u) + mq_unit_cost(KEYS);  // its first block (positions before: the start cost)
     x.ue = ld_uniform(a.mq_pre + u + 1);
     const int U1 = ld_uniform(a.upre + a.n_seqs);
     x.h = u / U1;
@@ -126,9 +130,9 @@ __device__ __forceinline__ Unit load_unit(const MultiQueryArgs &a, int u, int b)
 // Page of this wave's keys of block g of unit un (see issue_block).  (Read
 // a block ahead, at the end of the previous block, it measured 10 % slower
 // on config 4.)
-template <int WAVES>
+template <int WAVES, int KEYS>
 __device__ __forceinline__ int block_page(const Unit &un, int g, bool on, int wv) {
-    const int key0 = (g - un.ub) * kMqKeys + kMqKeys / WAVES * wv;
+    const int key0 = (g - un.ub) * KEYS + KEYS / WAVES * wv;
     return on ? ld_uniform(un.trow + (min(key0, un.ctx - 1) >> 4)) : 0;
 }
 
@@ -139,11 +143,12 @@ __device__ __forceinline__ int block_page(const Unit &un, int g, bool on, int wv
 // data; the mask drops them).  A disabled issue (past the workgroup's share)
 // goes through an empty resource: no memory access, but the same loads, so
 // every wave's load counter advances alike.
-template <int WAVES>
+template <int WAVES, int KEYS>
 __device__ __forceinline__ void issue_block(uint8_t *st, const MultiQueryArgs &a, const Unit &un, int g, bool on,
                                             int page, int wv, int lane, int row_bytes) {
-    constexpr int kPer = kMqKeys / WAVES;
-    const int key0 = (g - un.ub) * kMqKeys + kPer * wv;  // key of the unit
+    constexpr int kPer = KEYS / WAVES;
+    static_assert(kPer <= kBlockTokens && kBlockTokens % kPer == 0, "a wave's keys of a block lie in one page");
+    const int key0 = (g - un.ub) * KEYS + kPer * wv;  // key of the unit
     const int last = un.ctx - 1;
     const size_t off = (static_cast<size_t>(page) * kBlockTokens * row_bytes + un.h * kRowBytes) / 2;
     const uint32_t n = on ? kBlockTokens * row_bytes : 0u;
@@ -155,14 +160,15 @@ __device__ __forceinline__ void issue_block(uint8_t *st, const MultiQueryArgs &a
         const int row = min(key0 + 2 * i + (lane >> 5), last) & 15;
         const uint32_t dst = lds_addr(st + (kPer * wv / 2 + i) * kPairBytes);  // this load's two keys
         load_to_lds(rk, dst, row * row_bytes + 16 * k_granule(kl, q));
-        load_to_lds(rv, dst + kTileBytes, row * row_bytes + 16 * v_granule(kl, q));
+        load_to_lds(rv, dst + tile_bytes<KEYS>(), row * row_bytes + 16 * v_granule(kl, q));
     }
 }
 
-// Block i's loads have landed in LDS when at most the loads of blocks i+1
-// and i+2 (kMqKeys/WAVES loads each per wave) are outstanding.
-template <int WAVES>
-__device__ __forceinline__ void wait_block() { wait_vm<kMqKeys / WAVES * (kRing - 2)>(); }
+// Block i's loads have landed in LDS when at most the loads of the blocks
+// issued after it and before this wait (ring stages - 2 of them, KEYS/WAVES
+// loads each per wave) are outstanding.
+template <int WAVES, int KEYS>
+__device__ __forceinline__ void wait_block() { wait_vm<KEYS / WAVES * (ring_stages<KEYS>() - 2)>(); }
 
 __device__ __forceinline__ half8_t as_h8(uint4 v) { return __builtin_bit_cast(half8_t, v); }
 
@@ -181,8 +187,12 @@ __device__ __forceinline__ int mq_share_of(int i, int W) {
     return (W & 7) == 0 ? (i & 7) * (W >> 3) + (i >> 3) : i;
 }
 
-template <int NT, int WAVES, bool TREE>
+template <int NT, int WAVES, bool TREE, int KEYS>
 __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
+    constexpr int kRing = ring_stages<KEYS>();
+    constexpr int kTileBytes = tile_bytes<KEYS>();
+    constexpr int kKT = KEYS / 16;  // 16-key tiles of a block (QK)
+    constexpr int kKS = KEYS / 32;  // 32-key steps of a block (PV)
     __shared__ __attribute__((aligned(16))) uint8_t ring[kRing][2 * kTileBytes];
     const int w = mq_share_of(blockIdx.x, a.n_wg);  // this workgroup's share (and partial slots)
     const int W = a.n_wg;
@@ -214,16 +224,16 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
     // of the compute side, across unit boundaries.
     const int u0 = upper_index(a.mq_pre, a.n_units, q0, lane);
     const int U1 = ld_uniform(a.upre + a.n_seqs);
-    Unit iu = load_unit(a, u0, upper_index(a.upre, a.n_seqs, u0 % U1, lane));
+    Unit iu = load_unit<KEYS>(a, u0, upper_index(a.upre, a.n_seqs, u0 % U1, lane));
     int ig = max(q0, iu.ub);
     if (ig >= q1) return;  // the share holds only a unit's start cost
     int ipage = 0;  // page of the next issue
-    auto fetch_page = [&]() { ipage = block_page<WAVES>(iu, ig, ig < q1, wv); };
+    auto fetch_page = [&]() { ipage = block_page<WAVES, KEYS>(iu, ig, ig < q1, wv); };
     auto issue = [&](int slot) {
         const bool on = ig < q1;
-        issue_block<WAVES>(ring[slot], a, iu, ig, on, ipage, wv, lane, row_bytes);
+        issue_block<WAVES, KEYS>(ring[slot], a, iu, ig, on, ipage, wv, lane, row_bytes);
         if (on && ++ig < q1 && ig >= iu.ue) {
-            iu = load_unit(a, iu.u + 1, iu.b);
+            iu = load_unit<KEYS>(a, iu.u + 1, iu.b);
             ig = iu.ub;
         }
     };
@@ -277,7 +287,7 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
         }
 
         for (; g < seg_end; ++g) {
-            wait_block<WAVES>();
+            wait_block<WAVES, KEYS>();
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
             fetch_page();
@@ -285,12 +295,12 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             const uint8_t *kt = ring[n_done % kRing];
             const uint8_t *kbase = kt + key_off(col) + 16 * k_granule(col, grp);
-            const int key0 = (g - cu.ub) * kMqKeys;
+            const int key0 = (g - cu.ub) * KEYS;
 
             // S^T for keys key0 + 16*nt + 4*grp + i, row `col` of each tile.
-            float4_t s[NT][2];
+            float4_t s[NT][kKT];
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < kKT; ++nt) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) s[t][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
                 // key 16*nt + col, granule 4*kk + grp: kbase + nt*8 pairs + 64*kk
@@ -304,19 +314,19 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
                                                                         0, 0, 0);
                 }
             }
-            half8_t pb[NT];
+            half8_t pb[NT][kKS];
             float corr[NT];
             bool rescale = false;
             // A block wholly before the step's first new slot is visible to
             // every row (wave-uniform test); otherwise mask key by key.  Rows
             // past the unit's tokens are never written, so the open case
             // needs no mask at all.
-            const bool open = key0 + kMqKeys <= cu.ns;
+            const bool open = key0 + KEYS <= cu.ns;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 float mx = -INFINITY;
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
+                for (int nt = 0; nt < kKT; ++nt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         float v = s[t][nt][i] * scale;
@@ -347,9 +357,9 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
                 const float mu = (mn == -INFINITY) ? 0.0f : mn;  // rows with nothing visible yet
                 corr[t] = __builtin_amdgcn_exp2f(m[t] - mu);
                 rescale = rescale || (jump && m[t] != -INFINITY);
-                uint32_t pk[4];
+                uint32_t pk[2 * kKT];
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt) {
+                for (int nt = 0; nt < kKT; ++nt) {
                     pk[2 * nt] = pack_h2(__builtin_amdgcn_exp2f(s[t][nt][0] - mu),
                                          __builtin_amdgcn_exp2f(s[t][nt][1] - mu));
                     pk[2 * nt + 1] = pack_h2(__builtin_amdgcn_exp2f(s[t][nt][2] - mu),
@@ -357,13 +367,15 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
                 }
                 // l sums the fp16 probabilities PV uses.
                 constexpr uint32_t kOnes = 0x3c003c00u;  // fp16 pair (1, 1)
-                float psum = dot2(pk[0], kOnes, 0.0f);
-                psum = dot2(pk[1], kOnes, psum);
-                psum = dot2(pk[2], kOnes, psum);
-                psum = dot2(pk[3], kOnes, psum);
+                float psum = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 2 * kKT; ++i) psum = dot2(pk[i], kOnes, psum);
                 l[t] = l[t] * corr[t] + psum;
                 m[t] = mn;
-                pb[t] = __builtin_bit_cast(half8_t, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+#pragma unroll
+                for (int ks = 0; ks < kKS; ++ks)
+                    pb[t][ks] = __builtin_bit_cast(half8_t, make_uint4(pk[4 * ks], pk[4 * ks + 1], pk[4 * ks + 2],
+                                                                      pk[4 * ks + 3]));
             }
             // Rescale only when some row's reference max moved (wave-uniform).
             if (__builtin_amdgcn_ballot_w64(rescale)) {
@@ -385,18 +397,21 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             const uint8_t *vbase[2] = {vb + 64 * (vr & 1), vb - 64 * (vr & 1)};
 #pragma unroll
             for (int dt = 0; dt < 16; ++dt) {
-                short4_t part[2];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const uint8_t *src = vbase[(dt >> 1) & 1] + 8 * hh * kPairBytes + 32 * dt;
-                    part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t *)src);
+                for (int ks = 0; ks < kKS; ++ks) {  // keys 32*ks ..: 16 pairs on
+                    short4_t part[2];
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const uint8_t *src = vbase[(dt >> 1) & 1] + (16 * ks + 8 * hh) * kPairBytes + 32 * dt;
+                        part[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_t *)src);
+                    }
+                    const uint2 v0 = __builtin_bit_cast(uint2, part[0]);
+                    const uint2 v1 = __builtin_bit_cast(uint2, part[1]);
+                    const half8_t va = __builtin_bit_cast(half8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+                        acc[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t][ks], acc[t][dt], 0, 0, 0);
                 }
-                const uint2 v0 = __builtin_bit_cast(uint2, part[0]);
-                const uint2 v1 = __builtin_bit_cast(uint2, part[1]);
-                const half8_t va = __builtin_bit_cast(half8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    acc[t][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t], acc[t][dt], 0, 0, 0);
             }
             ++n_done;
         }
@@ -435,7 +450,7 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             }
         }
         if (g >= q1) break;
-        cu = load_unit(a, cu.u + 1, cu.b);
+        cu = load_unit<KEYS>(a, cu.u + 1, cu.b);
         g = cu.ub;
         if (g >= q1) break;  // the share ends inside the next unit's start cost
     }
@@ -454,7 +469,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     constexpr int kMaxP = 4;  // pieces requested together
     const int u = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    const int ub = a.mq_pre[u] + kMqUnitCost;  // the unit's first block
+    const int ub = a.mq_pre[u] + mq_unit_cost(a.keys);  // the unit's first block
     const int ue = a.mq_pre[u + 1];
     // Head and tile index of unit u (head-major units), and its sequence:
     // the number of sequences whose tiles end at or before the tile.
@@ -548,10 +563,17 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
 
 template <int NT, int WAVES>
 hipError_t launch_mq(const MultiQueryArgs &a, hipStream_t s) {
-    if (a.tree)
-        hipLaunchKernelGGL((mq_kernel<NT, WAVES, true>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
-    else
-        hipLaunchKernelGGL((mq_kernel<NT, WAVES, false>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
+    // 64-key blocks only for eight-wave causal tiles (mq_keys_for).
+    const bool k64 = a.keys == 64 && WAVES == 8 && !a.tree;
+    if (a.keys != 32 && !k64) return hipErrorInvalidValue;
+    if (a.tree) {
+        hipLaunchKernelGGL((mq_kernel<NT, WAVES, true, 32>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
+    } else if (k64) {
+        if constexpr (WAVES == 8)
+            hipLaunchKernelGGL((mq_kernel<NT, WAVES, false, 64>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((mq_kernel<NT, WAVES, false, 32>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(mq_combine_kernel, dim3(a.n_units, WAVES * NT), dim3(256), 0, s, a);

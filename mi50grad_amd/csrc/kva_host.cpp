@@ -129,8 +129,9 @@ struct kva_cache {
     int32_t st_n_seqs = 0, st_n_tok = 0, st_max_ctx = 0, st_max_new = 0, st_max_pos = 0;
     int32_t st_total_pages = 0;  // pages of all sequences of the step
     int32_t st_mq_units = 0;     // (sequence, token tile, kv head) units
-    int32_t st_mq_blocks = 0;    // 32-key blocks of all multi-query units
+    int32_t st_mq_blocks = 0;    // key blocks (and unit start costs) of all multi-query units
     int32_t st_mq_waves = 4;     // waves per workgroup of the multi-query kernel
+    int32_t st_mq_keys = 32;     // keys per multi-query block (mq_keys_for)
     int32_t st_mq_q = 0;         // new tokens per unit tile
     size_t off_upre = 0, off_mqpre = 0;
     bool st_all_one = false, st_has_bits = false;
@@ -735,15 +736,17 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
         tiles_all += (n_new[b] + mq_q - 1) / mq_q;
     }
     p_upre[n_seqs] = static_cast<int32_t>(tiles_all);
+    const int32_t mq_keys = kva::mq_keys_for(mq_waves, tree_bits != nullptr);
+    const int32_t unit_cost = kva::mq_unit_cost(mq_keys);
     int64_t units = 0, blocks = 0;
     for (int32_t hh = 0; hh < c->cfg.num_kv_heads; ++hh) {
         for (int32_t b = 0; b < n_seqs; ++b) {
             const int32_t tiles = (n_new[b] + mq_q - 1) / mq_q;
             for (int32_t tl = 0; tl < tiles; ++tl) {
                 const int64_t keys = tree_bits ? p_ctx[b] : p_start[b] + std::min(n_new[b], (tl + 1) * mq_q);
-                const int64_t nb = (keys + kva::kMqKeys - 1) / kva::kMqKeys;
+                const int64_t nb = (keys + mq_keys - 1) / mq_keys;
                 p_mqpre[units++] = static_cast<int32_t>(blocks);
-                blocks += kva::kMqUnitCost + nb;
+                blocks += unit_cost + nb;
             }
         }
     }
@@ -777,6 +780,7 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->st_mq_units = static_cast<int32_t>(units);
     c->st_mq_blocks = static_cast<int32_t>(blocks);
     c->st_mq_waves = mq_waves;
+    c->st_mq_keys = mq_keys;
     c->st_mq_q = mq_q;
     c->off_upre = o_upre;
     c->off_mqpre = o_mqpre;
@@ -1349,9 +1353,11 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     a.n_seqs = c->st_n_seqs;
     a.n_units = c->st_mq_units;
     a.total_blocks = c->st_mq_blocks;
-    // Stream-K share: one workgroup per CU, at least 4 key blocks each.
-    a.n_wg = static_cast<int32_t>(
-        std::max<int64_t>(1, std::min<int64_t>(c->mq_max_wg, (c->st_mq_blocks + 3) / 4)));
+    a.keys = c->st_mq_keys;
+    // Stream-K share: one workgroup per CU, at least 128 keys' blocks each.
+    const int64_t min_blocks = 128 / c->st_mq_keys;
+    a.n_wg = static_cast<int32_t>(std::max<int64_t>(
+        1, std::min<int64_t>(c->mq_max_wg, (c->st_mq_blocks + min_blocks - 1) / min_blocks)));
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
     a.tree = tree ? 1 : 0;

@@ -212,10 +212,11 @@ struct MultiQueryArgs {
     const int32_t *tok_off;   // device [n_seqs+1]: new-token ranges
     const uint64_t *tok_bits; // device [T] (tree mode) or null
     const int32_t *upre;      // device [n_seqs+1]: tiles of earlier sequences (units of one head)
-    const int32_t *mq_pre;    // device [n_units+1]: positions of earlier units (blocks + kMqUnitCost each)
+    const int32_t *mq_pre;    // device [n_units+1]: positions of earlier units (blocks + mq_unit_cost each)
     int32_t n_seqs;
     int32_t n_units;          // (kv head, sequence, token tile) units, head-major
-    int32_t total_blocks;     // positions of all units (blocks + kMqUnitCost each)
+    int32_t total_blocks;     // positions of all units (blocks + mq_unit_cost each)
+    int32_t keys;             // keys per block: mq_keys_for(n_waves, the step has tree bits)
     int32_t n_wg;             // workgroups sharing the blocks (stream-K)
     int32_t num_heads;
     int32_t num_kv_heads;
@@ -230,15 +231,21 @@ struct MultiQueryArgs {
     const uint16_t *gate;
     int64_t gate_stride;
 };
-constexpr int kMqKeys = 32;       // keys per multi-query block
-// The stream-K split of the multi-query kernel counts each unit as this many
-// blocks more than it has (the cost of starting a unit: its query rows,
-// its output), so a share full of short units gets fewer blocks.  Unit u's
-// blocks sit at positions [mq_pre[u] + kMqUnitCost, mq_pre[u+1]).  Four:
-// a unit start measured about two blocks' time, but with two the shares
-// holding many short units still ended last (config 4: 2 -> 132 us, 3 -> 122,
-// 4 -> 116, 5 and 6 -> 116-117).
-constexpr int kMqUnitCost = 4;
+// Keys per multi-query block.  64 for a step of eight-wave prefill tiles
+// (half the barriers, page lookups and softmax reductions per key, two LDS
+// stages of 66 KB: config 4 115.5 -> 110.4 us per call); 32 otherwise, a
+// four-stage ring that keeps 96 KB in flight for the HBM-bound tree verify
+// (config 5 at 64 keys: 862 -> 888 us) and for small steps.  A step planned
+// with tree bits uses 32 for kva_prefill too.
+constexpr int mq_keys_for(int waves, bool tree_plan) { return (waves == 8 && !tree_plan) ? 64 : 32; }
+// The stream-K split of the multi-query kernel counts each unit as the
+// blocks of 128 more keys than it has (the cost of starting a unit: its
+// query rows, its output), so a share full of short units gets fewer
+// blocks.  Unit u's blocks sit at positions [mq_pre[u] + cost, mq_pre[u+1]).
+// 128 keys: a unit start measured about two 32-key blocks' time, but with
+// two the shares holding many short units still ended last (config 4 at 32
+// keys per block, cost 2 -> 132 us, 3 -> 122, 4 -> 116, 5 and 6 -> 116-117).
+constexpr int mq_unit_cost(int keys) { return 128 / keys; }
 constexpr int kMqMaxGroup = 8;    // largest GQA group of the multi-query kernel
 constexpr int kMqSlotRows = 128;  // query rows of a partial slot (waves x 16 x tiles at most)
 // A unit's query rows are (token, head) pairs of the GQA group, 16 per

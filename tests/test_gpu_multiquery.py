@@ -31,9 +31,11 @@ def _ids(rng, nblk):
 
 
 def run_prefilled(device, prefix, chunk, num_heads=H, num_kv_heads=HKV, seed=0, scale=1.0,
-                  tree_parents=None):
+                  tree_parents=None, causal_on_tree_step=False):
     """Cache rows [0, prefix+chunk) pre-filled with random K/V (no append);
-    attention of the chunk's queries through kva_prefill / kva_tree_verify."""
+    attention of the chunk's queries through kva_prefill / kva_tree_verify
+    (causal_on_tree_step: kva_prefill on a step begun with the tree's bits,
+    compared with the causal rule)."""
     rng = np.random.default_rng(seed)
     B = len(prefix)
     total = [p + c for p, c in zip(prefix, chunk)]
@@ -51,14 +53,17 @@ def run_prefilled(device, prefix, chunk, num_heads=H, num_kv_heads=HKV, seed=0, 
     else:
         bits = tr.tree_bits(tree_parents) * B
         cache.begin_step(list(range(B)), chunk, tree_bits=bits)
-        cache.tree_verify(0, dq, out)
+        if causal_on_tree_step:
+            cache.prefill(0, dq, out)
+        else:
+            cache.tree_verify(0, dq, out)
     device.synchronize()
     got = out.numpy()
     exp = np.zeros((T, num_heads, D), np.float32)
     t = 0
     for b in range(B):
         n = chunk[b]
-        if tree_parents is None:
+        if tree_parents is None or causal_on_tree_step:
             exp[t:t + n] = orc.chunk_attention(q[t:t + n], kr[0][b], vr[0][b], prefix[b])
         else:
             P = prefix[b]
@@ -153,6 +158,25 @@ def test_chain_tree_equals_causal_prefill(device):
     causal_out, _ = run_prefilled(device, [300, 50], [7, 7], seed=9)
     assert max_err(tree_out, exp) <= TOL
     assert max_err(tree_out, causal_out) <= 1e-3
+
+
+def test_prefill_block_sizes(device):
+    """An eight-wave prefill step plans 64-key blocks; kva_prefill on a step
+    begun with tree bits runs the same causal rule on 32-key blocks, and the
+    tree kernel verifies the chain tree on 32-key blocks: all three agree
+    with the causal oracle, each other within its bar.  Contexts cover a
+    block's end exactly (64, 128 rows) and one past it."""
+    parents = [-1] + list(range(39))  # a chain of 40: 240 query rows, eight-wave tiles
+    prefix, chunk = [24, 88, 0, 1000, 985], [40] * 5
+    say("prefill block sizes")
+    plain, exp = run_prefilled(device, prefix, chunk, seed=11)
+    on_tree, exp_t = run_prefilled(device, prefix, chunk, seed=11, tree_parents=parents,
+                                   causal_on_tree_step=True)
+    tree_out, _ = run_prefilled(device, prefix, chunk, seed=11, tree_parents=parents)
+    assert max_err(plain, exp) <= TOL
+    assert max_err(on_tree, exp_t) <= TOL
+    assert max_err(tree_out, exp) <= TOL
+    assert max_err(plain, on_tree) <= 1e-3
 
 
 def test_tree_verify_append_then_rollback(device):
