@@ -918,7 +918,7 @@ def workload_line(dev, args) -> dict:
             "tok_per_s": r["tokens"] * r["steps"] / r["wall_s"],
             "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("prefill_c4_traffic.json"),
-                         "kernel": "kva_prefill = mq_kernel<1 tile, 8 waves, causal> + mq_combine_kernel",
+                         "kernel": "kva_prefill = mq_kernel<1 tile, 8 waves, causal, 64-key blocks> + mq_combine_kernel",
                          "avg_us": r["prefill_avg_us"], "alg_flops_per_launch": r["flops_per_layer"],
                          "alg_bytes_per_launch": r["bytes_per_layer"], "mfma_busy": stored_mfma_busy(),
                          "peak_derived": mfma_peak_derived()}})
@@ -935,7 +935,7 @@ def workload_line(dev, args) -> dict:
             "rollback_avg_us": r["rollback_avg_us"],
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("tree_c5_traffic.json"),
-                         "kernel": "kva_tree_verify = mq_kernel<1 tile, 4 waves, tree> + mq_combine_kernel",
+                         "kernel": "kva_tree_verify = mq_kernel<1 tile, 4 waves, tree, 32-key blocks> + mq_combine_kernel",
                          "avg_us": r["verify_avg_us"], "alg_bytes_per_launch": r["alg_bytes_per_layer"]}})
     raise ValueError(args.workload)
 
