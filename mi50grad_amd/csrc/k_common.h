@@ -24,6 +24,16 @@ __device__ __forceinline__ float hi_f(uint32_t w) { return h2f(static_cast<uint1
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
     return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
 }
+// The same rounding in one v_cvt_pk_f16_f32 (gfx950), for softmax
+// probabilities.  Outputs keep pack_h2: built with the vector form there,
+// the gated prefill's outputs measured up to 2 ulps from the gate applied
+// to the ungated outputs (1 with pack_h2), the compiled epilogues no longer
+// rounding alike.
+__device__ __forceinline__ uint32_t pack_p2(float lo, float hi) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t v = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+}
 
 // v_dot2_f32_f16: acc + a.lo*b.lo + a.hi*b.hi, fp16 pairs packed in dwords.
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {

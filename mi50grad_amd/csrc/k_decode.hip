@@ -188,7 +188,7 @@ __device__ __forceinline__ void compute_half(WaveState<G> &st, const HalfPage &p
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const float off = -mn[g] * qk_scale;
-        pa[g] = pack_h2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[g][0], qk_scale, off)),
+        pa[g] = pack_p2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[g][0], qk_scale, off)),
                         __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][1], qk_scale, off)));
         st.l[g] = dot2(pa[g], kOnes, st.l[g]);  // l sums the fp16 probabilities PV uses
     }
@@ -398,9 +398,9 @@ __device__ __forceinline__ void compute_page(MfmaState<G> &st, const Page &p, co
         st.m = mn;
     }
     const float off = -st.m * qk_scale;
-    const uint32_t pk0 = pack_h2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[0], qk_scale, off)),
+    const uint32_t pk0 = pack_p2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[0], qk_scale, off)),
                                  __builtin_amdgcn_exp2f(__builtin_fmaf(s[1], qk_scale, off)));
-    const uint32_t pk1 = pack_h2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2], qk_scale, off)),
+    const uint32_t pk1 = pack_p2(__builtin_amdgcn_exp2f(__builtin_fmaf(s[2], qk_scale, off)),
                                  __builtin_amdgcn_exp2f(__builtin_fmaf(s[3], qk_scale, off)));
     st.l = dot2(pk1, kOnes, dot2(pk0, kOnes, st.l));  // l sums the fp16 probabilities PV uses
     // Rows 4grp, 4grp+1 are pair 2grp; rows 4grp+2, 4grp+3 pair 2grp+1.  The

@@ -324,32 +324,37 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
             const bool open = key0 + KEYS <= cu.ns;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                float mx = -INFINITY;
+                // Masked scores become -inf; the max is taken over the raw
+                // scores and scaled once (scale > 0 keeps the order and the
+                // rounding of the largest), and the probabilities below
+                // fold the scale into one fma.
+                if (!open) {  // wave-uniform: blocks of the cache prefix skip this
 #pragma unroll
-                for (int nt = 0; nt < kKT; ++nt)
+                    for (int nt = 0; nt < kKT; ++nt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float v = s[t][nt][i] * scale;
-                        if (!open) {
-                            const int key = key0 + 16 * nt + 4 * grp + i;
+                        for (int i = 0; i < 4; ++i) {
                             bool vis;
                             if constexpr (TREE) {
                                 // The cache before the step, then the new rows
                                 // in the node's bit set (bits only for the
                                 // step's nodes, so keys past the sequence drop
                                 // out).  Bitwise, so no lane branches.
-                                const int rel = key - cu.ns;
+                                const int rel = key0 + 16 * nt + 4 * grp + i - cu.ns;
                                 const bool bit = ((qbits[t] >> (rel & 63)) & 1ull) != 0;
                                 vis = qvalid[t] & ((rel < 0) | ((rel < 64) & bit));
                             } else {
-                                vis = qvalid[t] & (key <= qslot[t]);  // qslot < ctx
+                                // key0 + 16nt + 4grp + i <= qslot (qslot < ctx)
+                                vis = qvalid[t] & (16 * nt + i <= qslot[t] - key0 - 4 * grp);
                             }
-                            v = vis ? v : -INFINITY;
+                            s[t][nt][i] = vis ? s[t][nt][i] : -INFINITY;
                         }
-                        s[t][nt][i] = v;
-                        mx = fmaxf(mx, v);
-                    }
-                mx = group4_max(mx);
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int nt = 0; nt < kKT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[t][nt][i]);
+                mx = group4_max(mx) * scale;
                 // Move the reference max only on a jump past the slack (or
                 // from -inf, where acc and l are still zero).
                 const bool jump = mx > m[t] + kRescaleSlack;
@@ -360,10 +365,10 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
                 uint32_t pk[2 * kKT];
 #pragma unroll
                 for (int nt = 0; nt < kKT; ++nt) {
-                    pk[2 * nt] = pack_h2(__builtin_amdgcn_exp2f(s[t][nt][0] - mu),
-                                         __builtin_amdgcn_exp2f(s[t][nt][1] - mu));
-                    pk[2 * nt + 1] = pack_h2(__builtin_amdgcn_exp2f(s[t][nt][2] - mu),
-                                             __builtin_amdgcn_exp2f(s[t][nt][3] - mu));
+                    pk[2 * nt] = pack_p2(__builtin_amdgcn_exp2f(fmaf(s[t][nt][0], scale, -mu)),
+                                         __builtin_amdgcn_exp2f(fmaf(s[t][nt][1], scale, -mu)));
+                    pk[2 * nt + 1] = pack_p2(__builtin_amdgcn_exp2f(fmaf(s[t][nt][2], scale, -mu)),
+                                             __builtin_amdgcn_exp2f(fmaf(s[t][nt][3], scale, -mu)));
                 }
                 // l sums the fp16 probabilities PV uses.
                 constexpr uint32_t kOnes = 0x3c003c00u;  // fp16 pair (1, 1)
