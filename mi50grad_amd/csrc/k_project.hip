@@ -313,28 +313,34 @@ __global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
     const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
     const NormRopeIn nin = norm_rope_in<32>(hr < H ? a.q_w : a.k_w, cos_row, sin_row, a.half_rot, lane);
     // Every split's partial is loaded at once (splits past a.splits reread
-    // split 0 and are not added), then summed in split order.
+    // split 0 and are not added), then summed in split order; or the
+    // projection as the library GEMM rounded it.
     const size_t N = static_cast<size_t>(a.n_a) + a.n_b;
-    const size_t split_stride = static_cast<size_t>(a.n_tok) * N;
-    const float *p = a.part + static_cast<size_t>(tc) * N + static_cast<size_t>(hr) * kHeadDim + 8 * lane;
-    float4_t plo[kProjMaxSplits], phi[kProjMaxSplits];
-#pragma unroll
-    for (int s = 0; s < kProjMaxSplits; ++s) {
-        const float *ps = p + (s < a.splits ? s : 0) * split_stride;
-        plo[s] = *reinterpret_cast<const float4_t *>(ps);
-        phi[s] = *reinterpret_cast<const float4_t *>(ps + 4);
-    }
-    float4_t lo = plo[0], hi = phi[0];
-#pragma unroll
-    for (int s = 1; s < kProjMaxSplits; ++s) {
-        lo = s < a.splits ? lo + plo[s] : lo;
-        hi = s < a.splits ? hi + phi[s] : hi;
-    }
+    const size_t row_at = static_cast<size_t>(tc) * N + static_cast<size_t>(hr) * kHeadDim + 8 * lane;
     uint4 y;
-    y.x = pack_h2(lo[0], lo[1]);
-    y.y = pack_h2(lo[2], lo[3]);
-    y.z = pack_h2(hi[0], hi[1]);
-    y.w = pack_h2(hi[2], hi[3]);
+    if (a.part16) {
+        y = ld16(a.part16 + row_at);
+    } else {
+        const size_t split_stride = static_cast<size_t>(a.n_tok) * N;
+        const float *p = a.part + row_at;
+        float4_t plo[kProjMaxSplits], phi[kProjMaxSplits];
+#pragma unroll
+        for (int s = 0; s < kProjMaxSplits; ++s) {
+            const float *ps = p + (s < a.splits ? s : 0) * split_stride;
+            plo[s] = *reinterpret_cast<const float4_t *>(ps);
+            phi[s] = *reinterpret_cast<const float4_t *>(ps + 4);
+        }
+        float4_t lo = plo[0], hi = phi[0];
+#pragma unroll
+        for (int s = 1; s < kProjMaxSplits; ++s) {
+            lo = s < a.splits ? lo + plo[s] : lo;
+            hi = s < a.splits ? hi + phi[s] : hi;
+        }
+        y.x = pack_h2(lo[0], lo[1]);
+        y.y = pack_h2(lo[2], lo[3]);
+        y.z = pack_h2(hi[0], hi[1]);
+        y.w = pack_h2(hi[2], hi[3]);
+    }
 
     if (hr < H) {
         const uint4 q = norm_rope_apply<32>(y, nin, a.half_rot, a.eps, lane);

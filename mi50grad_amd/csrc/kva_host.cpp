@@ -87,9 +87,9 @@ struct kva_cache {
     size_t proj_floats = 0;
     // Prefill-sized projections (steps of more than kProjTokens tokens): one
     // library GEMM per weight matrix over up to big_tokens tokens into
-    // d_proj_big [big_tokens][(2H+2Hkv)*256] fp32, then the finish kernel.
+    // d_proj_big [big_tokens][(2H+2Hkv)*256] fp16, then the finish kernel.
     // Set up on the first such call.
-    float *d_proj_big = nullptr;
+    uint16_t *d_proj_big = nullptr;
     int32_t big_tokens = 0;
     hipblasLtHandle_t lt = nullptr;
     void *lt_ws = nullptr;
@@ -856,9 +856,9 @@ static int32_t project_splits(const kva_cache *c, int32_t hidden, int32_t n_rows
     return best;
 }
 
-// Tokens of one library GEMM of a prefill-sized projection (its fp32 output
-// is [tokens][(2H+2Hkv)*256], 117 MB at 2048 tokens and 24 + 4 heads), and
-// the GEMM's workspace.
+// Tokens of one library GEMM of a prefill-sized projection (its output, fp16
+// rounded from fp32 sums, is [tokens][(2H+2Hkv)*256], 59 MB at 2048 tokens
+// and 24 + 4 heads), and the GEMM's workspace.
 constexpr int32_t kBigProjTokens = 2048;
 constexpr size_t kLtWorkspaceBytes = size_t(64) << 20;
 
@@ -871,7 +871,7 @@ static bool big_project_ready(kva_cache *c) {
     c->lt_tried = true;
     const int32_t tokens = std::min(c->cfg.max_step_tokens, kBigProjTokens);
     const size_t n = 2 * static_cast<size_t>(c->cfg.num_heads + c->cfg.num_kv_heads) * kva::kHeadDim;
-    if (hipMalloc(&c->d_proj_big, static_cast<size_t>(tokens) * n * sizeof(float)) != hipSuccess ||
+    if (hipMalloc(&c->d_proj_big, static_cast<size_t>(tokens) * n * sizeof(uint16_t)) != hipSuccess ||
         hipMalloc(&c->lt_ws, kLtWorkspaceBytes) != hipSuccess || hipblasLtCreate(&c->lt) != HIPBLAS_STATUS_SUCCESS) {
         (void)hipGetLastError();
         (void)hipFree(c->d_proj_big);
@@ -885,9 +885,10 @@ static bool big_project_ready(kva_cache *c) {
     return true;
 }
 
-// The plan of D[T][ldd] (fp32, N columns) = X[T][K] (fp16) . W[N][K]^T
-// (fp16): in the library's column-major terms D^T (N x T, ld ldd) = op(A) B
-// with A = W stored K x N (ld K) transposed and B = X stored K x T (ld K).
+// The plan of D[T][ldd] (fp16 from fp32 sums, N columns) = X[T][K] (fp16) .
+// W[N][K]^T (fp16): in the library's column-major terms D^T (N x T, ld ldd)
+// = op(A) B with A = W stored K x N (ld K) transposed and B = X stored K x T
+// (ld K).  The fp16 output is the projection the reference's GEMV stores.
 static kva_cache::LtPlan *lt_plan(kva_cache *c, int64_t T, int64_t N, int64_t K, int64_t ldd) {
     for (auto &pl : c->lt_plans)
         if (pl.T == T && pl.N == N && pl.K == K && pl.ldd == ldd) return &pl;
@@ -907,7 +908,7 @@ static kva_cache::LtPlan *lt_plan(kva_cache *c, int64_t T, int64_t N, int64_t K,
         hipblasLtMatmulDescSetAttribute(pl.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatrixLayoutCreate(&pl.la, HIP_R_16F, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatrixLayoutCreate(&pl.lb, HIP_R_16F, K, T, K) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&pl.lc, HIP_R_32F, N, T, ldd) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&pl.lc, HIP_R_16F, N, T, ldd) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
         hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws_max,
                                               sizeof(ws_max)) == HIPBLAS_STATUS_SUCCESS &&
@@ -990,13 +991,13 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
         if (ok) {
             const float one = 1.0f, zero = 0.0f;
             a.splits = 1;
-            a.part = c->d_proj_big;
+            a.part16 = c->d_proj_big;
             for (int32_t t0 = 0; t0 < c->st_n_tok; t0 += c->big_tokens) {
                 const int32_t n = std::min(c->big_tokens, c->st_n_tok - t0);
                 const uint16_t *xc = xs + static_cast<size_t>(t0) * hidden;
                 for (int m = 0; m < 2; ++m) {
                     const kva_cache::LtPlan *pl = lt_plan(c, n, m ? a.n_b : a.n_a, hidden, N);
-                    float *d = c->d_proj_big + (m ? a.n_a : 0);
+                    uint16_t *d = c->d_proj_big + (m ? a.n_a : 0);
                     const hipblasStatus_t st =
                         hipblasLtMatmul(c->lt, pl->op, &one, m ? a.w_b : a.w_a, pl->la, xc, pl->lb, &zero, d, pl->lc, d,
                                         pl->lc, &pl->algo, c->lt_ws, pl->ws, s);

@@ -69,6 +69,8 @@ struct ProjectArgs {
     int32_t n_tok;            // tokens of this chunk, 1..kProjTokens
     int32_t splits;
     float *part;              // [splits][n_tok][n_a + n_b]
+    const uint16_t *part16;   // or the projection already rounded to fp16,
+                              // [n_tok][n_a + n_b] (the library GEMM's output)
     int32_t tok0;             // the chunk's first token within the step
     uint16_t *q_out;          // [T][H][256]: normalised + rotated Q
     uint16_t *gate_out;       // [T][H][256]: Q_gate as projected (nullable)
