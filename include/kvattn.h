@@ -184,8 +184,8 @@ int kva_project_append(kva_cache *cache, int32_t layer, const void *x, int32_t h
  * 64 tokens through libkvattn's projection kernels (the weights are read
  * once per 64 tokens); larger steps through one hipBLASLt GEMM per weight
  * matrix over up to 2048 tokens (the reference's batched prefill GEMMs,
- * engine.py:3051-3068), then the same finish kernel (fp16 rounding, norm,
- * RoPE, append).  A larger step goes through the projection kernels when
+ * engine.py:3051-3068) that round the fp32 sums to fp16 on output, then
+ * the same finish kernel (norm, RoPE, append).  A larger step goes through the projection kernels when
  * the GEMM cannot be set up (first call while a graph is being recorded,
  * no device memory for its 64 MB workspace and 2048-token output, or no
  * library solution for the shape): the results satisfy the same contract
