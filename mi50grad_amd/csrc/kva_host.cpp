@@ -1405,6 +1405,9 @@ int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int
     std::vector<uint8_t> seen(c->cfg.max_seqs, 0);
     std::vector<int32_t> moves;
     std::vector<int32_t> move_off(1, 0);
+    // Everything is checked, and the upload sized, before any length changes:
+    // a refused call leaves the cache as it was.
+    size_t n_moves_all = 0, n_groups_all = 0;
     for (int32_t b = 0; b < n_seqs; ++b) {
         const int32_t s = seq_ids[b];
         int rc = check_seq(c, s);
@@ -1417,15 +1420,23 @@ int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int
         if (base_len[b] < 0 || base_len[b] > c->len[s])
             return fail(KVA_ERR_ROLLBACK, "sequence %d: base length %d outside [0, %d]", s, base_len[b], c->len[s]);
         int32_t prev = -1;
+        size_t n_moved = 0;
         for (int32_t j = 0; j < n; ++j) {
             const int32_t row = keep_rows[keep_off[b] + j];
             if (row <= prev) return fail(KVA_ERR_ROLLBACK, "keep_rows of sequence %d not strictly increasing", s);
             if (static_cast<int64_t>(base_len[b]) + row >= c->len[s])
                 return fail(KVA_ERR_ROLLBACK, "sequence %d: kept row %d beyond length %d", s,
                             base_len[b] + row, c->len[s]);
+            n_moved += row != j;
             prev = row;
         }
+        n_moves_all += n_moved;
+        n_groups_all += n_moved > 0;
     }
+    if (n_moves_all > 0 &&
+        round_up(n_moves_all * 3 * sizeof(int32_t), 16) + (n_groups_all + 1) * sizeof(int32_t) > c->aux_bytes)
+        return fail(KVA_ERR_CAPACITY, "rollback moves %zu rows, more than the staging area holds (%zu bytes)",
+                    n_moves_all, c->aux_bytes);
     for (int32_t b = 0; b < n_seqs; ++b) {
         const int32_t s = seq_ids[b];
         const int32_t n = keep_off[b + 1] - keep_off[b];
@@ -1443,8 +1454,7 @@ int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int
     const int32_t n_groups = static_cast<int32_t>(move_off.size()) - 1;
     const size_t bytes_moves = moves.size() * sizeof(int32_t);
     const size_t o_off = round_up(bytes_moves, 16);
-    const size_t total = o_off + move_off.size() * sizeof(int32_t);
-    if (total > c->aux_bytes) return fail(KVA_ERR_CAPACITY, "rollback moves exceed the staging area");
+    const size_t total = o_off + move_off.size() * sizeof(int32_t);  // fits: checked above
     hipStream_t st = static_cast<hipStream_t>(stream);
     uint8_t *h;
     int idx;

@@ -152,6 +152,23 @@ def test_rollback_validation_and_lengths():
     assert c.seq_len(0) == 23
 
 
+def test_rollback_beyond_staging_leaves_lengths():
+    """A rollback whose row moves do not fit the staging area (4096 moves at
+    this configuration) is refused before any length changes, also when a
+    valid sequence precedes the one that overflows."""
+    c = make(max_blocks=600, max_blocks_per_seq=300)
+    c.reserve(0, 4800)
+    c.set_len(0, 4800)
+    c.reserve(1, 32)
+    c.set_len(1, 32)
+    with pytest.raises(KvaError) as e:
+        c.rollback([1, 0], [16, 0], [[1, 3], list(range(1, 4800))])   # 4799 moves of sequence 0
+    assert code(e) == -5
+    assert c.seq_len(0) == 4800 and c.seq_len(1) == 32
+    c.rollback([1, 0], [16, 0], [[1, 3], list(range(1, 4001))])      # 4002 moves fit
+    assert c.seq_len(0) == 4000 and c.seq_len(1) == 18
+
+
 def test_set_len_bounds():
     c = make()
     c.reserve(0, 20)
