@@ -18,8 +18,16 @@
  *     and projection partials, the step plan) shared by every call on it,
  *     so two calls on one cache that overlap on different streams race:
  *     use one stream per cache, or one cache per stream;
- *   - the library allocates device memory only in kva_create and the
- *     kva_dev_* helpers, never inside a hot-path call.
+ *   - the library allocates device memory in kva_create and the kva_dev_*
+ *     helpers, plus two named exceptions: the first prefill-sized
+ *     kva_project_append on a cache (more than 64 tokens, outside a
+ *     recording) sets up its library GEMM once (a 2048-token fp16 output
+ *     and a 64 MB workspace), and kva_timeline_enable allocates the
+ *     timeline buffer.  No other call allocates; kva_legacy_decode_noalloc
+ *     allocates nothing at all;
+ *   - every call validates its arguments before it touches the device, so a
+ *     host-only cache (KVA_FLAG_HOST_ONLY) reports the same refusals and
+ *     answers a call that would pass them with KVA_ERR_NO_DEVICE.
  *
  * Reference citations are to larkinwc/mi50grad (file:line).
  */
@@ -345,9 +353,10 @@ int kva_legacy_qknorm_rope(void *x, const void *w, const void *cos_row,
 /* flash_attn_256_decode semantics (flash_attn_256_tuned.hip:198-350) on a
  * contiguous cache K/V [kv_seq_len, num_kv_heads, 256]: one query row
  * q [num_heads, 256] -> out [num_heads, 256].  `ws` (nullable) lends its
- * split-K workspace and split setting; with NULL the call runs the
- * whole-sequence form at every length (one workgroup per kv head: meant for
- * short caches; long ones take a workspace or kva_legacy_decode_noalloc).  */
+ * split-K workspace and split setting.  With NULL the call runs the
+ * whole-sequence form, which needs no workspace, and so takes caches of at
+ * most 1024 rows: a longer one returns KVA_ERR_STATE (give it a workspace,
+ * or call kva_legacy_decode_noalloc) instead of streaming on a few CUs.    */
 int kva_legacy_decode(kva_cache *ws, const void *q, const void *k_base,
                       const void *v_base, void *out, int32_t kv_seq_len,
                       int32_t num_heads, int32_t num_kv_heads, kva_stream_t stream);

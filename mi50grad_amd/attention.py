@@ -77,17 +77,24 @@ class FullAttentionLaunchers:
         self.tp_size = tp_size
         self.kv_cache = kv_cache
         self._kva_stream = stream
-        _setup(self, max_seq_len, tp_size)
+        _setup(self, rope_table_rows(self, max_seq_len), tp_size)
 
     def _init_rope_tables(self, max_seq_len: int):
+        """cos/sin tables of max_seq_len rows (the recipe of engine.py:1025-
+        1046, so the fp16 bits are the reference's).  Tables this object
+        already holds (the engine's own, or an earlier install's) are freed
+        once the new ones are in place."""
         cfg = self.config
         cos, sin = rope_tables(max_seq_len, cfg.head_dim, cfg.partial_rotary_factor, cfg.rope_theta)
+        old = [p for p in (getattr(self, "d_cos", 0), getattr(self, "d_sin", 0)) if p]
         self.rotary_dim = int(cfg.head_dim * cfg.partial_rotary_factor)
         self.rope_rows = max_seq_len
         self.d_cos = self.device.malloc(cos.nbytes)
         self.d_sin = self.device.malloc(sin.nbytes)
         self.device.upload(self.d_cos, cos.tobytes())
         self.device.upload(self.d_sin, sin.tobytes())
+        for p in old:
+            self.device.free(p)
 
     def set_direct_kv_write(self, enabled: bool):
         self._direct_kv_write = bool(enabled)
@@ -335,6 +342,21 @@ def bind_methods(engine, names=ENGINE_METHODS, gemv: bool = False) -> None:
         setattr(engine, name, types.MethodType(getattr(FullAttentionLaunchers, name), engine))
 
 
+def rope_table_rows(engine, max_seq_len: int | None = None) -> int:
+    """Rows the RoPE tables of an installed engine need: every position any
+    of its callers can address.  That is the largest of `max_seq_len`, the
+    max_seq_len of the engine's KV cache (the reference's own KVCache has
+    one too, engine.py:91) or of the engine itself, and the rows of tables
+    already built (rope_rows): reference code indexes engine.d_cos directly
+    (engine.py:2741; tp_engine.py:169, 341, 2933) without a bounds check, so
+    the tables must never shrink.  2048 (the engine's default max_seq_len,
+    engine.py:475) when none of these is known."""
+    cands = (max_seq_len, getattr(getattr(engine, "kv_cache", None), "max_seq_len", None),
+             getattr(engine, "max_seq_len", None), getattr(engine, "rope_rows", None))
+    rows = max((int(c) for c in cands if c), default=0)
+    return rows if rows > 0 else 2048
+
+
 def install(engine, kv_cache: KVCache | None = None, max_seq_len: int | None = None, stream=None,
             gemv: bool = False):
     """Route an engine instance's full-attention calls through libkvattn.
@@ -346,12 +368,11 @@ def install(engine, kv_cache: KVCache | None = None, max_seq_len: int | None = N
     KVCache kept, the contiguous-cache launches still work (on a split-K
     workspace made here, once) but the paged ones (_prefill_full_attention)
     refuse.  Launches go to `stream` (None: the legacy default stream).
-    Returns the engine."""
+    The RoPE tables are rebuilt with rope_table_rows(engine, max_seq_len)
+    rows and the engine's previous tables freed.  Returns the engine."""
     if kv_cache is not None:
         engine.kv_cache = kv_cache
     engine._kva_stream = stream
-    own = getattr(engine, "kv_cache", None)
-    rows = max_seq_len or (own.max_seq_len if isinstance(own, KVCache) else 2048)
-    _setup(engine, rows, getattr(engine, "tp_size", 1))
+    _setup(engine, rope_table_rows(engine, max_seq_len), getattr(engine, "tp_size", 1))
     bind_methods(engine, gemv=gemv)
     return engine

@@ -59,6 +59,8 @@ constexpr int kMinPagesPerWg = 1;   // a short sequence still spreads over sever
 // many rows runs the whole-sequence form: one workgroup per sequence and kv
 // head, no partials and no combine launch.
 constexpr int kWholeMaxTokens = 1024;
+// The CU count a host-only cache validates against (MI355X).
+constexpr int kHostOnlyCus = 256;
 
 }  // namespace
 
@@ -371,6 +373,12 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
                                          sizeof(int32_t)),
                             256);
     c->stage_bytes = std::max(c->step_bytes, c->aux_bytes);
+    // Projection partials: every split of one launch pair's tokens.  Sized
+    // for host-only caches too, whose calls are validated exactly as on the
+    // device (against a nominal MI355X CU count) before they are refused.
+    c->proj_floats = static_cast<size_t>(kva::kProjMaxSplits) * kva::kProjTokens *
+                     (2 * static_cast<size_t>(cfg->num_heads) + 2 * cfg->num_kv_heads) * kva::kHeadDim;
+    c->n_cu = kHostOnlyCus;
     if (!c->host_only) {
         auto cleanup = [&](int code) {
             kva_destroy(c);
@@ -409,9 +417,6 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
             return cleanup(hip_fail(e, "hipMalloc(multi-query workspace)"));
         if ((e = hipMalloc(&c->d_mq_ml, mq_rows * 2 * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(multi-query workspace ml)"));
-        // Projection partials: every split of one launch pair's tokens.
-        c->proj_floats = static_cast<size_t>(kva::kProjMaxSplits) * kva::kProjTokens *
-                         (2 * static_cast<size_t>(cfg->num_heads) + 2 * cfg->num_kv_heads) * kva::kHeadDim;
         if ((e = hipMalloc(&c->d_proj, c->proj_floats * sizeof(float))) != hipSuccess)
             return cleanup(hip_fail(e, "hipMalloc(projection workspace)"));
         for (int i = 0; i < kStageSlots; ++i) {
@@ -831,13 +836,14 @@ static int make_append(kva_cache *c, int32_t layer, void *q, void *k, const void
 static int append_impl(kva_cache *c, int32_t layer, void *q, void *k, const void *v, const void *q_norm_w,
                        const void *k_norm_w, const void *cos_tab, const void *sin_tab, int32_t table_rows,
                        kva_stream_t stream) {
-    int rc = require_device(c);
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_layer(c, layer);
     if (rc) return rc;
-    if ((rc = check_layer(c, layer))) return rc;
     if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
-    if (c->st_n_tok == 0) return KVA_OK;
+    if (c->st_n_tok == 0) return require_device(c);
     kva::AppendArgs a;
     if ((rc = make_append(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, a))) return rc;
+    if ((rc = require_device(c))) return rc;
     KVA_HIP(kva::launch_append(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;
 }
@@ -928,11 +934,11 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
                         const void *w_kv_fused, const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
                         const void *sin_tab, int32_t table_rows, void *q_out, void *q_gate_out, void *kv_out,
                         kva_stream_t stream) {
-    int rc = require_device(c);
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_layer(c, layer);
     if (rc) return rc;
-    if ((rc = check_layer(c, layer))) return rc;
     if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
-    if (c->st_n_tok == 0) return KVA_OK;
+    if (c->st_n_tok == 0) return require_device(c);
     if (!x || !w_q_fused || !w_kv_fused || !q_norm_w || !k_norm_w || !cos_tab || !sin_tab || !q_out)
         return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (!aligned16(x) || !aligned16(w_q_fused) || !aligned16(w_kv_fused) || !aligned16(q_norm_w) ||
@@ -949,6 +955,7 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
     if (c->st_max_pos >= table_rows)
         return fail(KVA_ERR_INVALID_ARG, "RoPE position %d beyond the %d table rows", c->st_max_pos,
                     table_rows);
+    if ((rc = require_device(c))) return rc;
     kva::ProjectArgs a{};
     a.w_a = static_cast<const uint16_t *>(w_q_fused);
     a.w_b = static_cast<const uint16_t *>(w_kv_fused);
@@ -981,7 +988,7 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
     // tokens by a library GEMM (the reference's batched path at seq_len >= 32,
     // engine.py:3051-3068), not once per 64 tokens.  Every plan is made (and
     // checked) before anything is launched.
-    if (c->st_n_tok > kva::kProjTokens && big_project_ready(c)) {
+    if (c->st_n_tok > kva::kProjTokens && !c->capturing && big_project_ready(c)) {
         const int64_t N = static_cast<int64_t>(a.n_a) + a.n_b;
         bool ok = true;
         for (int32_t t0 = 0; t0 < c->st_n_tok && ok; t0 += c->big_tokens) {
@@ -1141,14 +1148,15 @@ static int check_gate(const void *gate, int64_t gate_stride, int32_t num_heads) 
 // runs the whole-sequence form, else launched first (k left unwritten).
 static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *gate, int64_t gate_stride,
                        void *out, kva_stream_t stream, const kva::AppendArgs *app = nullptr) {
-    int rc = require_device(c);
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_layer(c, layer);
     if (rc) return rc;
-    if ((rc = check_layer(c, layer))) return rc;
     if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
     if (!c->st_all_one) return fail(KVA_ERR_STATE, "kva_decode needs exactly one new token per sequence");
     if (!q || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (!aligned16(q) || !aligned16(out)) return fail(KVA_ERR_MISALIGNED, "q/out must be 16-byte aligned");
     if ((rc = check_gate(gate, gate_stride, c->cfg.num_heads))) return rc;
+    if ((rc = require_device(c))) return rc;
     kva::DecodeArgs a{};
     a.gate = static_cast<const uint16_t *>(gate);
     a.gate_stride = gate_stride;
@@ -1197,9 +1205,9 @@ static int append_decode_impl(kva_cache *c, int32_t layer, void *q, const void *
                               const void *q_norm_w, const void *k_norm_w, const void *cos_tab, const void *sin_tab,
                               int32_t table_rows, const void *gate, int64_t gate_stride, void *out,
                               kva_stream_t stream) {
-    int rc = require_device(c);
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_layer(c, layer);
     if (rc) return rc;
-    if ((rc = check_layer(c, layer))) return rc;
     if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
     if (!c->st_all_one) return fail(KVA_ERR_STATE, "kva_append_decode needs exactly one new token per sequence");
     kva::AppendArgs ap;
@@ -1261,10 +1269,9 @@ int kva_project_append(kva_cache *c, int32_t layer, const void *x, int32_t hidde
 
 static int out_project_impl(kva_cache *c, const void *attn, int32_t n_tok, int32_t q_dim, const void *w_o,
                             int32_t n_out, const void *residual, void *out, kva_stream_t stream) {
-    int rc = require_device(c);
-    if (rc) return rc;
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
     if (n_tok < 0) return fail(KVA_ERR_INVALID_ARG, "n_tok %d is negative", n_tok);
-    if (n_tok == 0) return KVA_OK;
+    if (n_tok == 0) return require_device(c);
     if (!attn || !w_o || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (!aligned16(attn) || !aligned16(w_o) || !aligned16(residual) || !aligned16(out))
         return fail(KVA_ERR_MISALIGNED, "attn, w_o, residual and out must be 16-byte aligned");
@@ -1289,6 +1296,7 @@ static int out_project_impl(kva_cache *c, const void *attn, int32_t n_tok, int32
     if (static_cast<size_t>(a.splits) * chunk_tok * n_out > c->proj_floats)
         return fail(KVA_ERR_INVALID_ARG, "n_out %d x %lld tokens exceeds the projection workspace (%zu floats)", n_out,
                     static_cast<long long>(chunk_tok), c->proj_floats);
+    if (int rc = require_device(c)) return rc;
     a.part = c->d_proj;
     a.y_out = static_cast<uint16_t *>(out);
     a.residual = static_cast<const uint16_t *>(residual);
@@ -1326,14 +1334,15 @@ int kva_decode_gated(kva_cache *c, int32_t layer, const void *q, const void *gat
 static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream,
                        bool tree, const void *gate = nullptr, int64_t gate_stride = 0) {
     if (int rc = refuse_while_capturing(c, tree ? "kva_tree_verify" : "kva_prefill")) return rc;
-    int rc = require_device(c);
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_layer(c, layer);
     if (rc) return rc;
-    if ((rc = check_layer(c, layer))) return rc;
     if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
     if (tree && !c->st_has_bits) return fail(KVA_ERR_STATE, "tree verify needs tree_bits in kva_step_begin");
     if (!q || !out) return fail(KVA_ERR_INVALID_ARG, "NULL tensor pointer");
     if (!aligned16(q) || !aligned16(out)) return fail(KVA_ERR_MISALIGNED, "q/out must be 16-byte aligned");
     if ((rc = check_gate(gate, gate_stride, c->cfg.num_heads))) return rc;
+    if ((rc = require_device(c))) return rc;
     if (c->st_n_tok == 0) return KVA_OK;
     kva::MultiQueryArgs a{};
     a.gate = static_cast<const uint16_t *>(gate);
@@ -1620,8 +1629,15 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
     // Every sequence has the same length: the page prefix sums are implicit.
     const int64_t unit_pages = (kv_seq_len + kva::kBlockTokens - 1) / kva::kBlockTokens;
     const int64_t pages = unit_pages * batch;
-    // Without a workspace (and not the allocation-free entry point) every
-    // length runs the whole-sequence form, which needs none.
+    // Without a workspace (and not the allocation-free entry point) only the
+    // whole-sequence form can run, which needs none: it gives each kv head
+    // one workgroup, so a long cache would stream on a few CUs.  Such calls
+    // are refused rather than run an order of magnitude below the split form.
+    if (!ws && !noalloc && kv_seq_len > kWholeMaxTokens)
+        return fail(KVA_ERR_STATE,
+                    "kv_seq_len %d > %d needs a workspace cache (ws) for its split-K partials, or "
+                    "kva_legacy_decode_noalloc",
+                    kv_seq_len, kWholeMaxTokens);
     if (noalloc && num_heads > kva::kNoAllocMaxHeads)
         return fail(KVA_ERR_CAPACITY, "num_heads %d: the static decode scratch (%zu bytes) serves at most %d heads",
                     num_heads, kva::kNoAllocScratchBytes, kva::kNoAllocMaxHeads);
@@ -1631,7 +1647,7 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
         KVA_HIP(hipGetDevice(&dev));
         KVA_HIP(hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev));
     }
-    if ((a.whole = use_whole(ws, ws ? ws->split_user : 0, (ws || noalloc) ? kv_seq_len : 0, batch, num_heads,
+    if ((a.whole = use_whole(ws, ws ? ws->split_user : 0, kv_seq_len, batch, num_heads,
                              num_kv_heads, std::max(1, n_cu)))) {
     } else if (noalloc) {
         void *scratch = nullptr;

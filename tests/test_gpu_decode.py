@@ -415,27 +415,3 @@ def test_append_decode_head_groups(device, B):
     assert max_err(out_t.numpy(), exp) <= TOL
     for c in (fused, twin):
         c.destroy()
-
-
-def test_append_decode_refusals(device):
-    """kva_append_decode needs a step of one new token per sequence and the
-    append's operands; refused on the host, before any launch."""
-    rng = np.random.default_rng(80)
-    cache, _, _ = build_cache([10, 20], [[0, 1], [2, 3]], extra_rows=3, rng=rng)
-    tables = Tables(device, 64)
-    q = device.array(np.zeros((3, H, D), np.float16))
-    k = device.array(np.zeros((3, HKV, D), np.float16))
-    v = device.array(np.zeros((3, HKV, D), np.float16))
-    w = device.array(np.ones(D, np.float16))
-    out = device.empty((3, H, D), np.float16)
-    say("append+decode refusals")
-    cache.begin_step([0, 1], [2, 1])
-    with pytest.raises(_lib.KvaError, match="one new token"):
-        cache.append_decode(0, q, k, v, w, w, tables.d_cos, tables.d_sin, tables.rows, out)
-    cache.begin_step([0, 1], [1, 1])
-    with pytest.raises(_lib.KvaError, match="table rows"):
-        cache.append_decode(0, q, k, v, w, w, tables.d_cos, tables.d_sin, 5, out)
-    with pytest.raises(_lib.KvaError, match="NULL gate"):
-        _lib.call("kva_append_decode_gated", cache.handle, 0, q.ptr, k.ptr, v.ptr, w.ptr, w.ptr, tables.d_cos.ptr,
-                  tables.d_sin.ptr, tables.rows, None, 0, out.ptr, None)
-    cache.destroy()

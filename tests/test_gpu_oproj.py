@@ -14,7 +14,6 @@ oracle (oracle.out_project).
 import numpy as np
 import pytest
 
-from mi50grad_amd import _lib
 from oracle import kvattn_oracle as orc
 
 from gpu_helpers import build_cache, say
@@ -80,29 +79,16 @@ def test_out_project_random_in_place(device):
     cache.destroy()
 
 
-def test_out_project_errors(device):
+def test_out_project_empty_and_residual(device):
+    """No rows is a no-op; two exact rows with the residual are bit-exact.
+    (The argument refusals are checked on a host-only cache in
+    test_host_logic.py, before any device work.)"""
     rng = np.random.default_rng(42)
-    say("out_project validation")
+    say("out_project empty + residual")
     cache = _cache()
     x, w, r = _inputs(rng, 2, 512, 64, True)
     dx, dw, dr = device.array(x), device.array(w), device.array(r)
     out = device.empty((2, 64), np.float16)
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
-        cache.out_project(dx, 2, 500, dw, 64, out)  # q_dim not a multiple of 512
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
-        cache.out_project(dx, 2, 512, dw, 60, out)  # n_out not a multiple of 16
-    # Beyond the projection workspace for 2 tokens (2 x n_out partial floats
-    # > its 3.67 M): refused on the host.  The size must exceed the check
-    # itself, not only the buffers: a call that passed the check would run
-    # the GEMM over n_out rows of these 64-row buffers.
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG.*workspace"):
-        cache.out_project(dx, 2, 512, dw, 1 << 24, out)
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
-        cache.out_project(dx, -1, 512, dw, 64, out)
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
-        cache.out_project(None, 2, 512, dw, 64, out)
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_MISALIGNED"):
-        cache.out_project(dx, 2, 512, dw, 64, out, residual=dr.ptr + 2)
     cache.out_project(dx, 0, 512, dw, 64, out)  # no rows: nothing to do
     cache.out_project(dx, 2, 512, dw, 64, out, residual=dr)
     device.synchronize()

@@ -20,7 +20,6 @@ append, against the oracle's producer (oracle.project_append).
 import numpy as np
 import pytest
 
-from mi50grad_amd import _lib
 from oracle import kvattn_oracle as orc
 
 from gpu_helpers import HKV, H, D, Tables, build_cache, max_err, say
@@ -210,11 +209,11 @@ def test_project_prefill_sized_step(device):
     cache.destroy()
 
 
-def test_project_optional_outputs_and_errors(device):
+def test_project_optional_outputs(device):
     rng = np.random.default_rng(34)
     lengths = [40, 7]
     ids = _ids(rng, [4, 2])
-    say("project_append optional outputs and validation")
+    say("project_append optional outputs")
     cache, kr, vr = build_cache(lengths, ids, extra_rows=[1, 1], rng=rng)
     tables = Tables(device, 128)
     wq, wkv, qw, kw = _weights(rng, 512, True)
@@ -222,21 +221,7 @@ def test_project_optional_outputs_and_errors(device):
     args = [device.array(x), 512, device.array(wq), device.array(wkv), device.array(qw), device.array(kw),
             tables.d_cos, tables.d_sin, tables.rows]
     q_out = device.empty((2, H, D), np.float16)
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_STATE"):
-        cache.project_append(0, *args, q_out)  # no step begun
     cache.begin_step([0, 1], [1, 1])
-    bad = list(args)
-    bad[1] = 1000
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
-        cache.project_append(0, *bad, q_out)
-    bad = list(args)
-    bad[0] = args[0].ptr + 2
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_MISALIGNED"):
-        cache.project_append(0, *bad, q_out)
-    bad = list(args)
-    bad[8] = 40  # RoPE table too short for position 40
-    with pytest.raises(_lib.KvaError, match="KVA_ERR_INVALID_ARG"):
-        cache.project_append(0, *bad, q_out)
     cache.project_append(0, *args, q_out)  # gate and kv outputs omitted
     device.synchronize()
     pos = [40, 7]

@@ -6,6 +6,7 @@ base, unsorted keep lists, call order.  No device memory is touched.
 """
 import pytest
 
+from mi50grad_amd import _lib
 from mi50grad_amd._lib import KvaError
 from mi50grad_amd.kv_cache import PagedKVCache
 
@@ -128,7 +129,12 @@ def test_tree_bits_validation():
 
 
 def test_hot_calls_need_a_device_and_a_step():
+    """Validation comes first (here: no step begun), then the device."""
     c = make()
+    with pytest.raises(KvaError) as e:
+        c.decode(0, 1 << 20, 1 << 20)
+    assert code(e) == -8
+    c.begin_step([0], [1])
     with pytest.raises(KvaError) as e:
         c.decode(0, 1 << 20, 1 << 20)
     assert code(e) == -3
@@ -211,3 +217,132 @@ def test_graph_recording_validation():
     with pytest.raises(KvaError) as e:
         _lib.call("kva_graph_destroy", None)
     assert code(e) == -1
+
+
+# ---- argument refusals of the device entry points, on a host-only cache ----
+# Every hot-path call validates its arguments before it touches the device,
+# so the refusals are checked here with fake (aligned, never dereferenced)
+# pointers; a call that passes every check answers KVA_ERR_NO_DEVICE.  The
+# GPU tests then only ever hand the device buffers that cover what they ask
+# for.
+FAKE = 1 << 20
+
+
+def _rows(c, seq_ids, lens):
+    for s, n in zip(seq_ids, lens):
+        c.reserve(s, n)
+        c.set_len(s, n)
+
+
+def test_out_project_refusals_before_device():
+    c = make(num_heads=24, num_kv_heads=4)
+    with pytest.raises(KvaError, match="q_dim 500") as e:
+        c.out_project(FAKE, 2, 500, FAKE, 64, FAKE)
+    assert code(e) == -1
+    with pytest.raises(KvaError, match="n_out 60") as e:
+        c.out_project(FAKE, 2, 512, FAKE, 60, FAKE)
+    assert code(e) == -1
+    # Beyond the projection workspace for 2 tokens: refused on the host.
+    with pytest.raises(KvaError, match="workspace") as e:
+        c.out_project(FAKE, 2, 512, FAKE, 1 << 24, FAKE)
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        c.out_project(FAKE, -1, 512, FAKE, 64, FAKE)
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        c.out_project(None, 2, 512, FAKE, 64, FAKE)
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        c.out_project(FAKE, 2, 512, FAKE, 64, FAKE, residual=FAKE + 2)
+    assert code(e) == -10
+    with pytest.raises(KvaError) as e:  # every check passed: only the device is missing
+        c.out_project(FAKE, 2, 512, FAKE, 64, FAKE, residual=FAKE)
+    assert code(e) == -3
+    # The widest output one token can take (an lm_head's) passes the checks.
+    with pytest.raises(KvaError) as e:
+        c.out_project(FAKE, 1, 512, FAKE, 151936, FAKE)
+    assert code(e) == -3
+    c.destroy()
+
+
+def test_project_append_refusals_before_device():
+    c = make(num_heads=24, num_kv_heads=4)
+    _rows(c, [0, 1], [40, 7])
+    args = [FAKE, 512, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 128]
+    with pytest.raises(KvaError) as e:
+        c.project_append(0, *args, FAKE)  # no step begun
+    assert code(e) == -8
+    c.begin_step([0, 1], [1, 1])
+    for i, val, want in ((1, 1000, -1), (0, FAKE + 2, -10), (8, 40, -1), (2, None, -1), (6, FAKE + 4, -10)):
+        bad = list(args)
+        bad[i] = val
+        with pytest.raises(KvaError) as e:
+            c.project_append(0, *bad, FAKE)
+        assert code(e) == want, (i, val)
+    with pytest.raises(KvaError) as e:
+        c.project_append(5, *args, FAKE)  # layer out of range
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        c.project_append(0, *args, FAKE)
+    assert code(e) == -3
+    c.destroy()
+
+
+def test_decode_and_append_refusals_before_device():
+    c = make(num_heads=24, num_kv_heads=4)
+    _rows(c, [0, 1], [10, 20])
+    c.begin_step([0, 1], [2, 1])
+    with pytest.raises(KvaError, match="one new token") as e:
+        c.decode(0, FAKE, FAKE)
+    assert code(e) == -8
+    with pytest.raises(KvaError, match="one new token"):
+        c.append_decode(0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, FAKE)
+    c.begin_step([0, 1], [1, 1])
+    with pytest.raises(KvaError, match="table rows"):
+        c.append_decode(0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 5, FAKE)
+    with pytest.raises(KvaError) as e:
+        c.append(0, FAKE, FAKE + 8, FAKE, FAKE, FAKE, FAKE, FAKE, 64)
+    assert code(e) == -10
+    with pytest.raises(KvaError) as e:
+        c.decode(0, FAKE, FAKE, gate=FAKE + 4)
+    assert code(e) == -10
+    with pytest.raises(KvaError) as e:
+        c.decode(0, FAKE, FAKE, gate=FAKE, gate_stride=24 * 256 - 4)
+    assert code(e) == -1
+    with pytest.raises(KvaError, match="NULL gate"):
+        _lib.call("kva_append_decode_gated", c.handle, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, None, 0,
+                  FAKE, None)
+    for call in (lambda: c.decode(0, FAKE, FAKE), lambda: c.append(0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64),
+                 lambda: c.append_decode(0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, FAKE)):
+        with pytest.raises(KvaError) as e:
+            call()
+        assert code(e) == -3
+    c.destroy()
+
+
+def test_multi_query_refusals_before_device():
+    c = make(num_heads=24, num_kv_heads=4)
+    _rows(c, [0], [10])
+    c.begin_step([0], [3])
+    with pytest.raises(KvaError, match="tree_bits") as e:
+        c.tree_verify(0, FAKE, FAKE)
+    assert code(e) == -8
+    with pytest.raises(KvaError) as e:
+        c.prefill(0, FAKE + 2, FAKE)
+    assert code(e) == -10
+    with pytest.raises(KvaError) as e:
+        c.prefill(0, FAKE, FAKE)
+    assert code(e) == -3
+    c.destroy()
+
+
+def test_legacy_decode_without_workspace_refuses_long_caches():
+    """kva_legacy_decode with no workspace cache runs only the whole-sequence
+    form; past 1024 rows it refuses (KVA_ERR_STATE) instead of streaming a
+    long cache on one workgroup per kv head.  Refused before any launch."""
+    with pytest.raises(KvaError, match="workspace") as e:
+        _lib.call("kva_legacy_decode", None, FAKE, FAKE, FAKE, FAKE, 1025, 24, 4, None)
+    assert code(e) == -8
+    with pytest.raises(KvaError, match="workspace") as e:
+        _lib.call("kva_legacy_decode_batched", None, FAKE, FAKE, FAKE, FAKE, 5000, 2, 5000 * 2048, 24, 4, None)
+    assert code(e) == -8

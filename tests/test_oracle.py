@@ -41,6 +41,19 @@ def test_rope_table_hash_full_range():
         f"(this numpy: {np.__version__})")
 
 
+def test_product_rope_table_hash_full_range():
+    """The tables the product uploads (mi50grad_amd.rope.rope_tables, used by
+    attention._init_rope_tables and the GPU tests' cos/sin) are pinned to the
+    same golden digest over rows 0..32776, the positions configs 3 and 5
+    reach, not only through the oracle's restatement."""
+    from mi50grad_amd.rope import rope_tables, table_digest
+
+    g = golden()
+    cos, sin = rope_tables(g["rope_rows"])
+    assert cos.shape == (g["rope_rows"], 32)
+    assert table_digest(cos, sin) == g["rope_sha256"]
+
+
 def test_rope_table_closed_form():
     cos, sin = orc.rope_tables(4096)
     # Position 0 is the identity rotation.
