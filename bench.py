@@ -154,17 +154,23 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
     seqs = list(range(B))
     ones = [1] * B
 
-    def step(ev_pairs=None):
+    def step(ev_pairs=None, kernel=False):
+        # ev_pairs: per layer, events around the kva_decode call, or (kernel)
+        # the library's events around the decode kernel alone.
         for b in seqs:
             cache.set_len(b, int(lengths[b]))
         cache.begin_step(seqs, ones)
         for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
             cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
-            if ev_pairs is not None:
+            if ev_pairs is not None and kernel:
+                cache.kernel_events(ev_pairs[layer][0], ev_pairs[layer][1])
+            elif ev_pairs is not None:
                 ev_pairs[layer][0].record()
             cache.decode(layer, q, out)
-            if ev_pairs is not None:
+            if ev_pairs is not None and not kernel:
                 ev_pairs[layer][1].record()
+        if kernel:
+            cache.kernel_events(None, None)
 
     log(f"{label}: B={B} sum_ctx={int(np.sum(lengths)) + B} warmup={warmup}")
     for _ in range(warmup):
@@ -178,11 +184,19 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
     dev.synchronize()
     wall = time.perf_counter() - t0
     dec_ms = [e[0].elapsed_ms(e[1]) for per_step in evs for e in per_step]
+    # The decode kernel's own duration, in steps of their own: two more event
+    # markers inside each call add a few us to it, so they stay out of the
+    # steps the call bracket and the step time come from.
+    for i in range(steps):
+        step(evs[i], kernel=True)
+    dev.synchronize()
+    ker_ms = [e[0].elapsed_ms(e[1]) for per_step in evs for e in per_step]
     for per_step in evs:
-        for a, b in per_step:
-            a.destroy()
-            b.destroy()
-    log(f"{label}: {steps} steps in {wall * 1e3:.2f} ms; decode kernel avg {np.mean(dec_ms) * 1e3:.1f} us")
+        for pair in per_step:
+            for x in pair:
+                x.destroy()
+    log(f"{label}: {steps} steps in {wall * 1e3:.2f} ms; kva_decode avg {np.mean(dec_ms) * 1e3:.1f} us, "
+        f"decode kernel avg {np.mean(ker_ms) * 1e3:.1f} us")
     tl = None
     if timeline:
         # Outside the timed region: one more step, each layer's decode
@@ -213,6 +227,7 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
         "kv_bytes_per_layer": by["kv"], "alg_bytes_decode_launch": by["kv"] + by["q"],
         "alg_bytes_layer_step": by["kv"] + by["q"] + by["out"] + by["append"],
         "decode_avg_us": float(np.mean(dec_ms) * 1e3), "decode_min_us": float(np.min(dec_ms) * 1e3),
+        "kernel_avg_us": float(np.mean(ker_ms) * 1e3),
         "split_tokens": split_used, "n_splits": n_splits, "timeline": tl,
     }
 
@@ -587,17 +602,21 @@ def c4_workload(dev, steps, warmup):
     inputs = make_inputs(dev, T)
     seqs = list(range(B))
 
-    def step(evs=None):
+    def step(evs=None, kernel=False):
         for b in seqs:
             cache.set_len(b, prefix[b])
         cache.begin_step(seqs, chunk)
         for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
             cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
-            if evs is not None:
+            if evs is not None and kernel:
+                cache.kernel_events(evs[layer][0], evs[layer][1])  # mq_kernel alone
+            elif evs is not None:
                 evs[layer][0].record()
             cache.prefill(layer, q, out)
-            if evs is not None:
+            if evs is not None and not kernel:
                 evs[layer][1].record()
+        if kernel:
+            cache.kernel_events(None, None)
 
     for _ in range(warmup):
         step()
@@ -612,12 +631,21 @@ def c4_workload(dev, steps, warmup):
         dev.synchronize()
         wall += time.perf_counter() - t0
     ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s]
+    for i in range(steps):  # mq_kernel's own duration, in steps of their own
+        flush()
+        step(evs[i], kernel=True)
+        dev.synchronize()
+    kms = [e[0].elapsed_ms(e[1]) for s in evs for e in s]
+    for s in evs:
+        for pair in s:
+            for x in pair:
+                x.destroy()
     flush.free()
     cache.destroy()
     flops = 4 * H * D * sum(sum(p + i + 1 for i in range(c)) for p, c in zip(prefix, chunk))
     by = (sum(p + c for p, c in zip(prefix, chunk)) * ROW_BYTES + 2 * T * H * D * 2)
     return {"wall_s": wall, "steps": steps, "tokens": T, "flops_per_layer": flops, "bytes_per_layer": by,
-            "prefill_avg_us": float(np.mean(ms) * 1e3)}
+            "prefill_avg_us": float(np.mean(ms) * 1e3), "kernel_avg_us": float(np.mean(kms) * 1e3)}
 
 
 def c5_workload(dev, steps, warmup, layers=4, batch=64):
@@ -652,17 +680,21 @@ def c5_workload(dev, steps, warmup, layers=4, batch=64):
     keep = [tr.root_to_node_path(wl.C5_PARENTS, int(n)) for n in accept]
     seqs = list(range(batch))
 
-    def step(evs=None):
+    def step(evs=None, kernel=False):
         for b in seqs:
             cache.set_len(b, lengths[b])
         cache.begin_step(seqs, [9] * batch, rope_pos=rope_pos, tree_bits=bits)
         for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
             cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
-            if evs is not None:
+            if evs is not None and kernel:
+                cache.kernel_events(evs[layer][0], evs[layer][1])  # mq_kernel alone
+            elif evs is not None:
                 evs[layer][0].record()
             cache.tree_verify(layer, q, out)
-            if evs is not None:
+            if evs is not None and not kernel:
                 evs[layer][1].record()
+        if kernel:
+            cache.kernel_events(None, None)
         if evs is not None:
             evs[layers][0].record()
         cache.rollback(seqs, lengths, keep)
@@ -680,10 +712,19 @@ def c5_workload(dev, steps, warmup, layers=4, batch=64):
     wall = time.perf_counter() - t0
     verify_ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s[:layers]]
     rb_ms = [s[layers][0].elapsed_ms(s[layers][1]) for s in evs]
+    for i in range(steps):  # mq_kernel's own duration, in steps of their own
+        step(evs[i], kernel=True)
+    dev.synchronize()
+    kernel_ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s[:layers]]
+    for s in evs:
+        for pair in s:
+            for x in pair:
+                x.destroy()
     cache.destroy()
     kv = sum(lengths) * ROW_BYTES + T * ROW_BYTES
     return {"wall_s": wall, "steps": steps, "layers": layers, "kv_bytes_per_layer": kv,
             "alg_bytes_per_layer": kv + 2 * T * H * D * 2, "verify_avg_us": float(np.mean(verify_ms) * 1e3),
+            "kernel_avg_us": float(np.mean(kernel_ms) * 1e3),
             "rollback_avg_us": float(np.mean(rb_ms) * 1e3), "sum_len": sum(lengths)}
 
 
@@ -927,6 +968,7 @@ def workload_line(dev, args) -> dict:
     if args.workload == "c4":
         r = c4_workload(dev, args.steps, args.warmup)
         tflops = r["flops_per_layer"] / (r["prefill_avg_us"] * 1e-6) / 1e12
+        kernel_tflops = r["flops_per_layer"] / (r["kernel_avg_us"] * 1e-6) / 1e12
         ms = r["wall_s"] * 1e3 / r["steps"]
         extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c4()}
         return ({**extra, 
@@ -938,12 +980,17 @@ def workload_line(dev, args) -> dict:
             "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("prefill_c4_traffic.json"),
                          "kernel": "kva_prefill = mq_kernel<1 tile, 8 waves, causal, 64-key blocks> + mq_combine_kernel",
+                         "mq_kernel": {"what": "mq_kernel alone: HIP events the library records around its launch "
+                                               "(kva_kernel_events), in a second set of as many steps",
+                                       "avg_us": r["kernel_avg_us"], "achieved": kernel_tflops,
+                                       "frac": kernel_tflops / MFMA_PEAK_TFLOPS},
                          "avg_us": r["prefill_avg_us"], "alg_flops_per_launch": r["flops_per_layer"],
                          "alg_bytes_per_launch": r["bytes_per_layer"], "mfma_busy": stored_mfma_busy(),
                          "peak_derived": mfma_peak_derived()}})
     if args.workload == "c5":
         r = c5_workload(dev, args.steps, args.warmup)
         gbs = r["alg_bytes_per_layer"] / (r["verify_avg_us"] * 1e-6) / 1e9
+        kernel_gbs = r["alg_bytes_per_layer"] / (r["kernel_avg_us"] * 1e-6) / 1e9
         ms = r["wall_s"] * 1e3 / r["steps"]
         extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c5()}
         return ({**extra, 
@@ -955,6 +1002,10 @@ def workload_line(dev, args) -> dict:
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("tree_c5_traffic.json"),
                          "kernel": "kva_tree_verify = mq_kernel<1 tile, 4 waves, tree, 32-key blocks> + mq_combine_kernel",
+                         "mq_kernel": {"what": "mq_kernel alone: HIP events the library records around its launch "
+                                               "(kva_kernel_events), in a second set of as many steps",
+                                       "avg_us": r["kernel_avg_us"], "achieved": kernel_gbs,
+                                       "frac": kernel_gbs / HBM_PEAK_GBS},
                          "avg_us": r["verify_avg_us"], "alg_bytes_per_launch": r["alg_bytes_per_layer"]}})
     raise ValueError(args.workload)
 
@@ -990,7 +1041,7 @@ def main() -> int:
         line["ctx8192"] = {k: sub[k] for k in ("value", "unit", "pct_of_hbm_peak", "tok_per_s", "ms_per_step")}
         line["ctx8192"]["config"] = sub["config"]["workload"]
         line["ctx8192"]["roofline"] = {k: sub["roofline"][k] for k in ("achieved", "frac", "avg_us",
-                                                                         "alg_bytes_per_launch")}
+                                                                         "alg_bytes_per_launch", "decode_kernel")}
         rd, cp = read_probe(dev), copy_probe(dev)
         line["peaks"] = {
             "vendor_hbm_gbs": HBM_PEAK_GBS,
@@ -1018,8 +1069,12 @@ def other_configs(dev, args) -> dict:
                          "two_calls_us_per_step": d["two_calls_per_layer"]["step_us"],
                          "launches_per_step": d["launches_per_step"], "timing": d["timing"]},
         "c4": lambda d: {"tflops": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
+                         "mq_kernel_frac": d["roofline"]["mq_kernel"]["frac"],
+                         "mq_kernel_avg_us": d["roofline"]["mq_kernel"]["avg_us"],
                          "tok_per_s": d["tok_per_s"], "mfma_busy": d["roofline"]["mfma_busy"]},
         "c5": lambda d: {"gbs": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
+                         "mq_kernel_frac": d["roofline"]["mq_kernel"]["frac"],
+                         "mq_kernel_avg_us": d["roofline"]["mq_kernel"]["avg_us"],
                          "rollback_avg_us": d["rollback_avg_us"]},
         "proj": lambda d: {"gbs": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
                            "out_project_avg_us": d["out_project"]["avg_us"],
@@ -1058,6 +1113,7 @@ def decode_line(dev, which, args):
     value = kv_total / r["wall_s"] / 1e9
     ms_step = r["wall_s"] * 1e3 / r["steps"]
     achieved = r["alg_bytes_decode_launch"] / (r["decode_avg_us"] * 1e-6) / 1e9
+    kernel_gbs = r["alg_bytes_decode_launch"] / (r["kernel_avg_us"] * 1e-6) / 1e9
     traffic_file = f"decode_{which}_traffic.json"
     return {
         "metric": "decode-attn KV-read HBM GB/s (% of MI355X peak) + tok/s at B=32, ctx=8192",
@@ -1079,7 +1135,12 @@ def decode_line(dev, which, args):
                      "kernel": "kva_decode = decode_mfma_kernel<6> (stream-K, QK on MFMA) + combine_kernel<6> (one stream, "
                                "HIP events around the call)",
                      "avg_us": r["decode_avg_us"],
-                     "alg_bytes_per_launch": r["alg_bytes_decode_launch"]},
+                     "alg_bytes_per_launch": r["alg_bytes_decode_launch"],
+                     "decode_kernel": {"what": "decode_mfma_kernel<6> alone: HIP events the library records right "
+                                               "before and after its launch (kva_kernel_events), in a second set of "
+                                               "as many steps",
+                                       "avg_us": r["kernel_avg_us"], "achieved": kernel_gbs,
+                                       "frac": kernel_gbs / HBM_PEAK_GBS}},
     }
 
 

@@ -312,6 +312,19 @@ int kva_get_decode_split(const kva_cache *cache, int32_t *split_tokens,
  * in the whole-sequence form records its workgroups (n_wg of them,
  * grid_rows = 1; several per sequence and kv head), each with its
  * sequence's page count.  Off by default; costs one device buffer while on. */
+/* Dominant-kernel timing (no counterpart in the reference, which times
+ * perf_counter around a device sync, bench_optimization_baseline.py:54-69).
+ * While set, each following hot-path call on this cache records `before` on
+ * its stream right before its main kernel and `after` right after it, so
+ * kva_event_elapsed_ms(before, after) is that kernel's own duration: the
+ * decode kernel of kva_decode / kva_append_decode (without the combine
+ * launch or the append), mq_kernel of kva_prefill / kva_tree_verify
+ * (without its combine), the GEMM of kva_project_append / kva_out_project
+ * (without the finish kernel).  A call that launches its main kernel more
+ * than once (chunked projections) records around each, so the events hold
+ * the last.  Both NULL: off.  Refused while a graph is being recorded.     */
+int kva_kernel_events(kva_cache *cache, kva_event_t before, kva_event_t after);
+
 int kva_timeline_enable(kva_cache *cache, int32_t on);
 int kva_timeline_read(const kva_cache *cache, uint64_t *dst, size_t cap_words,
                       int32_t *n_wg, int32_t *grid_rows);

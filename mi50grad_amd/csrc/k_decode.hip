@@ -962,15 +962,21 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     }
 }
 
+// The caller's timing events around the decode kernel itself (if any).
+hipError_t mark(hipEvent_t ev, hipStream_t s) { return ev ? hipEventRecord(ev, s) : hipSuccess; }
+
 template <int GP>
 hipError_t launch_whole(const DecodeArgs &a, hipStream_t s) {
     const int units8 = (a.n_seqs * a.num_kv_heads + 7) / 8;
     const dim3 grid(units8 * 8 * a.whole), block(64 * kWholeWaves);
+    hipError_t e = mark(a.ev_before, s);
+    if (e != hipSuccess) return e;
     if (a.fused)
         hipLaunchKernelGGL((whole_kernel<GP, true>), grid, block, 0, s, a);
     else
         hipLaunchKernelGGL((whole_kernel<GP, false>), grid, block, 0, s, a);
-    return hipGetLastError();
+    e = hipGetLastError();
+    return e != hipSuccess ? e : mark(a.ev_after, s);
 }
 
 template <int G>
@@ -980,9 +986,10 @@ hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
     // the rest.
     int hpw = a.num_kv_heads <= kMfmaWaves ? a.num_kv_heads : kMfmaWaves;
     while (a.num_kv_heads % hpw) --hpw;
-    hipLaunchKernelGGL(decode_mfma_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(64 * hpw), 0, s, a);
-    hipError_t e = hipGetLastError();
+    hipError_t e = mark(a.ev_before, s);
     if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(decode_mfma_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(64 * hpw), 0, s, a);
+    if ((e = hipGetLastError()) != hipSuccess || (e = mark(a.ev_after, s)) != hipSuccess) return e;
     hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * kCombineWaves), 0, s, a);
     return hipGetLastError();
 }

@@ -571,6 +571,10 @@ hipError_t launch_mq(const MultiQueryArgs &a, hipStream_t s) {
     // 64-key blocks only for eight-wave causal tiles (mq_keys_for).
     const bool k64 = a.keys == 64 && WAVES == 8 && !a.tree;
     if (a.keys != 32 && !k64) return hipErrorInvalidValue;
+    if (a.ev_before) {
+        const hipError_t e = hipEventRecord(a.ev_before, s);
+        if (e != hipSuccess) return e;
+    }
     if (a.tree) {
         hipLaunchKernelGGL((mq_kernel<NT, WAVES, true, 32>), dim3(a.n_wg), dim3(64 * WAVES), 0, s, a);
     } else if (k64) {
@@ -581,6 +585,7 @@ hipError_t launch_mq(const MultiQueryArgs &a, hipStream_t s) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (a.ev_after && (e = hipEventRecord(a.ev_after, s)) != hipSuccess) return e;
     hipLaunchKernelGGL(mq_combine_kernel, dim3(a.n_units, WAVES * NT), dim3(256), 0, s, a);
     return hipGetLastError();
 }

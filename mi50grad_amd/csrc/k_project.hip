@@ -431,9 +431,20 @@ hipError_t launch_proj_gemm(const ProjectArgs &a, hipStream_t s) {
 
 }  // namespace
 
+// The GEMM of a launch pair between the caller's timing events (if any).
+hipError_t launch_proj_gemm_timed(const ProjectArgs &a, hipStream_t s) {
+    if (a.ev_before) {
+        const hipError_t e = hipEventRecord(a.ev_before, s);
+        if (e != hipSuccess) return e;
+    }
+    const hipError_t e = launch_proj_gemm(a, s);
+    if (e != hipSuccess || !a.ev_after) return e;
+    return hipEventRecord(a.ev_after, s);
+}
+
 hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
     if (a.n_tok <= 0) return hipSuccess;
-    const hipError_t e = launch_proj_gemm(a, s);
+    const hipError_t e = launch_proj_gemm_timed(a, s);
     if (e != hipSuccess) return e;
     const int blocks_per_tok = (2 * a.num_heads + 2 * a.num_kv_heads + 7) / 8;
     hipLaunchKernelGGL(proj_finish_kernel, dim3(a.n_tok * blocks_per_tok), dim3(256), 0, s, a);
@@ -450,7 +461,7 @@ hipError_t launch_project_finish(const ProjectArgs &a, hipStream_t s) {
 hipError_t launch_out_project(const ProjectArgs &a, hipStream_t s) {
     if (a.n_tok <= 0) return hipSuccess;
     if (a.n_b != 0 || a.n_a % 16 != 0) return hipErrorInvalidValue;
-    const hipError_t e = launch_proj_gemm(a, s);
+    const hipError_t e = launch_proj_gemm_timed(a, s);
     if (e != hipSuccess) return e;
     const int threads = a.n_tok * (a.n_a / 8);
     hipLaunchKernelGGL(oproj_finish_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, a);

@@ -140,6 +140,10 @@ struct kva_cache {
     size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
            off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0;
 
+    // Caller's timing events around the dominant kernel of each hot call
+    // (kva_kernel_events); null: none.
+    hipEvent_t kev_before = nullptr, kev_after = nullptr;
+
     int32_t split_user = 0;  // decode tokens per workgroup (0 = automatic)
     int32_t last_split = 0, last_nwg = 0;
     bool last_whole = false;  // the last decode ran the whole-sequence form
@@ -982,6 +986,8 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
     a.num_kv_heads = c->cfg.num_kv_heads;
     a.half_rot = half_rot;
     a.eps = c->cfg.eps;
+    a.ev_before = c->kev_before;
+    a.ev_after = c->kev_after;
     const auto *xs = static_cast<const uint16_t *>(x);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     // Prefill-sized steps: the weights are read once per kBigProjTokens
@@ -1002,6 +1008,7 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
             for (int32_t t0 = 0; t0 < c->st_n_tok; t0 += c->big_tokens) {
                 const int32_t n = std::min(c->big_tokens, c->st_n_tok - t0);
                 const uint16_t *xc = xs + static_cast<size_t>(t0) * hidden;
+                if (c->kev_before) KVA_HIP(hipEventRecord(c->kev_before, s));
                 for (int m = 0; m < 2; ++m) {
                     const kva_cache::LtPlan *pl = lt_plan(c, n, m ? a.n_b : a.n_a, hidden, N);
                     uint16_t *d = c->d_proj_big + (m ? a.n_a : 0);
@@ -1011,6 +1018,7 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
                     if (st != HIPBLAS_STATUS_SUCCESS)
                         return fail(KVA_ERR_INVALID_ARG, "hipblasLtMatmul failed (status %d)", static_cast<int>(st));
                 }
+                if (c->kev_after) KVA_HIP(hipEventRecord(c->kev_after, s));
                 a.tok0 = t0;
                 a.n_tok = n;
                 a.x = xc;
@@ -1085,6 +1093,17 @@ int kva_timeline_read(const kva_cache *c, uint64_t *dst, size_t cap_words, int32
     if (cap_words < words) return fail(KVA_ERR_CAPACITY, "timeline needs %zu words, %zu given", words, cap_words);
     KVA_HIP(hipDeviceSynchronize());
     KVA_HIP(hipMemcpy(dst, c->d_timeline, words * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    return KVA_OK;
+}
+
+int kva_kernel_events(kva_cache *c, kva_event_t before, kva_event_t after) {
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    if ((before == nullptr) != (after == nullptr))
+        return fail(KVA_ERR_INVALID_ARG, "give both events or neither");
+    if (int rc = refuse_while_capturing(c, "kva_kernel_events")) return rc;
+    if (before && c->host_only) return fail(KVA_ERR_NO_DEVICE, "cache was created host-only");
+    c->kev_before = static_cast<hipEvent_t>(before);
+    c->kev_after = static_cast<hipEvent_t>(after);
     return KVA_OK;
 }
 
@@ -1187,6 +1206,8 @@ static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *g
         a.min_pages = kMinPagesPerWg;
     }
     a.out = static_cast<uint16_t *>(out);
+    a.ev_before = c->kev_before;
+    a.ev_after = c->kev_after;
     if (app) {
         kva::AppendArgs ap = *app;
         ap.keep_k = 1;
@@ -1298,6 +1319,8 @@ static int out_project_impl(kva_cache *c, const void *attn, int32_t n_tok, int32
                     static_cast<long long>(chunk_tok), c->proj_floats);
     if (int rc = require_device(c)) return rc;
     a.part = c->d_proj;
+    a.ev_before = c->kev_before;
+    a.ev_after = c->kev_after;
     a.y_out = static_cast<uint16_t *>(out);
     a.residual = static_cast<const uint16_t *>(residual);
     const auto *xs = static_cast<const uint16_t *>(attn);
@@ -1376,6 +1399,8 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     a.q_tile = c->st_mq_q;
     a.ws_acc = c->d_mq_acc;
     a.ws_ml = c->d_mq_ml;
+    a.ev_before = c->kev_before;
+    a.ev_after = c->kev_after;
     const hipError_t e = kva::launch_multi_query(a, static_cast<hipStream_t>(stream));
     if (e == hipErrorNotSupported)
         return fail(KVA_ERR_UNSUPPORTED, "multi-query attention kernel not available for this shape");

@@ -94,6 +94,9 @@ struct ProjectArgs {
     // fp16(x W_o^T + residual), both [T][n_a]; residual nullable, may be y_out.
     uint16_t *y_out;
     const uint16_t *residual;
+    // Events around the GEMM kernel of a launch pair (null: none), as in
+    // DecodeArgs.
+    hipEvent_t ev_before, ev_after;
 };
 hipError_t launch_project(const ProjectArgs &a, hipStream_t s);
 // The finish kernel alone, over a.n_tok tokens of a.part (splits partials
@@ -153,6 +156,9 @@ struct DecodeArgs {
     // of G / whole query heads): no partials, no combine; the stream-K
     // fields are unused.  G / whole must be 1, 2, 3, 4, 6 or 8.
     int32_t whole;
+    // Events recorded on the stream right before and after the decode
+    // kernel itself (null: none): the dominant kernel's own duration.
+    hipEvent_t ev_before, ev_after;
     // 1 (whole form only): the step's append is done in the same launch
     // from `app` (one new token per sequence, token b of sequence b): each
     // workgroup normalises and rotates its query rows (written back in
@@ -232,6 +238,8 @@ struct MultiQueryArgs {
     // query head hq at gate + t*gate_stride + hq*256.
     const uint16_t *gate;
     int64_t gate_stride;
+    // Events around mq_kernel itself (null: none), as in DecodeArgs.
+    hipEvent_t ev_before, ev_after;
 };
 // Keys per multi-query block.  64 for a step of eight-wave prefill tiles
 // (half the barriers, page lookups and softmax reductions per key, two LDS

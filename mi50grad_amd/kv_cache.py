@@ -241,6 +241,12 @@ class PagedKVCache:
         _lib.call("kva_get_decode_split", self.handle, ctypes.byref(s), ctypes.byref(n))
         return s.value, n.value
 
+    def kernel_events(self, before=None, after=None) -> None:
+        """Record Events `before` / `after` around the main kernel of each
+        following hot-path call (kva_kernel_events); None, None: off."""
+        _lib.call("kva_kernel_events", self.handle, before.handle if before else None,
+                  after.handle if after else None)
+
     def timeline_enable(self, on: bool = True) -> None:
         """Record per-wave timestamps in every decode launch (kva_timeline_enable)."""
         _lib.call("kva_timeline_enable", self.handle, 1 if on else 0)
