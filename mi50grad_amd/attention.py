@@ -11,6 +11,8 @@ engine code calls them unchanged:
 * ``_launch_decode_attn_256``       engine.py:2760-2804 (flash_attn_256_decode)
 * ``_launch_decode_attn_256_batched`` engine.py:2806-2857
 * ``_prefill_full_attention``       engine.py:3043-3139
+* ``_decode_full_attention``        engine.py:1943-2092
+* ``_decode_full_attention_batched`` engine.py:1778-1876
 * ``build_decode_launch_cache``     engine.py:3309-3555 (its qknorm_q, qknorm_k
   and decode_attn entries, with the same mutable parameter indices)
 * ``rollback_kv_cache``             tp_engine.py:1673-1687
@@ -191,18 +193,28 @@ class FullAttentionLaunchers:
                              "after k_weight)")
         return wq, wkv
 
-    def _prefill_step(self, layer_idx: int, seq_len: int) -> None:
-        """Begin the paged step for a prefill once, at its first full-attention
-        layer; later layers of the same prefill reuse it (every layer appends
-        the same slots at the same positions)."""
+    def _paged_kv(self, what: str) -> KVCache:
+        if not isinstance(self.kv_cache, KVCache):
+            raise ValueError(f"{what} needs a mi50grad_amd KVCache (the paged cache whose steps it appends to)")
+        return self.kv_cache
+
+    def _paged_step(self, layer_idx: int, n_new: int, lens: list[int], rope_pos: list[int] | None = None) -> None:
+        """Begin the paged step of an engine step once, at its first
+        full-attention layer: batch slots 0..len(lens)-1 hold lens[b] rows
+        and append n_new each (RoPE positions rope_pos, default the slots).
+        Later layers of the same engine step reuse it (every layer appends
+        the same slots at the same positions); a layer seen again, or other
+        lengths or positions, begin a new one."""
         kv = self.kv_cache
-        key = (kv.current_len, seq_len)
-        if getattr(self, "_pf_key", None) != key or layer_idx in self._pf_layers:
-            kv.paged.set_len(0, kv.current_len)
-            kv.paged.begin_step([0], [seq_len], stream=self._kva_stream)
-            self._pf_key = key
-            self._pf_layers = set()
-        self._pf_layers.add(layer_idx)
+        key = (tuple(lens), n_new, tuple(rope_pos) if rope_pos is not None else None)
+        if getattr(self, "_step_key", None) != key or layer_idx in self._step_layers:
+            for b, n in enumerate(lens):
+                kv.paged.set_len(b, n)
+            pos = None if rope_pos is None else [p + i for p in rope_pos for i in range(n_new)]
+            kv.paged.begin_step(list(range(len(lens))), [n_new] * len(lens), rope_pos=pos, stream=self._kva_stream)
+            self._step_key = key
+            self._step_layers = set()
+        self._step_layers.add(layer_idx)
 
     def _prefill_full_attention(self, layer_idx: int, lw, seq_len: int):
         """Full-attention prefill of seq_len tokens of batch slot 0
@@ -222,16 +234,14 @@ class FullAttentionLaunchers:
         it; the reference's prefill starts from an empty cache, which is the
         current_len = 0 case.  The caller sets current_len afterwards, as
         prefill_step does (engine.py:3283)."""
-        if not isinstance(self.kv_cache, KVCache):
-            raise ValueError("_prefill_full_attention needs a mi50grad_amd KVCache (the paged cache "
-                             "whose steps it appends to)")
+        self._paged_kv("_prefill_full_attention")
         cfg = self.config
         h = cfg.hidden_size
         q_dim = self.local_num_attention_heads * cfg.head_dim
         wq, wkv = self._stacked_weights(lw)
         for t in range(seq_len):
             self._launch_rmsnorm(self.d_pf_normed + t * h * 2, self.d_pf_hidden + t * h * 2, lw.attn_norm, h)
-        self._prefill_step(layer_idx, seq_len)
+        self._paged_step(layer_idx, seq_len, [self.kv_cache.current_len])
         paged = self.kv_cache.paged
         layer = self.kv_cache._full_layer_slot(layer_idx)
         paged.project_append(layer, self.d_pf_normed, h, wq, wkv, lw.q_norm, lw.k_norm, self.d_cos,
@@ -241,6 +251,77 @@ class FullAttentionLaunchers:
                       gate_stride=q_dim)
         paged.out_project(self.d_pf_attn_out, seq_len, q_dim, lw.o_weight, h, self.d_pf_hidden,
                           residual=self.d_pf_hidden, stream=self._kva_stream)
+
+    # ---- decode (engine.py:1778-1876, 1943-2092) ------------------------------
+    def _decode_full_attention(self, layer_idx: int, lw, position: int):
+        """Full-attention decode of batch slot 0 (engine.py:1943-2092), FP16
+        attention weights, d_hidden updated in place.
+
+        The engine has RMS-normed the hidden state into d_normed.  Through
+        libkvattn: the Q/Q_gate/K/V projection with QK-norm + RoPE at
+        `position` and the K/V append into the cache row current_len
+        (kva_project_append: Q -> d_q, Q_gate -> d_q_gate, K and V as
+        projected -> d_kv_fused), decode attention over current_len + 1 rows
+        with the sigmoid gate of _launch_sigmoid_mul (engine.py:2055-2056)
+        fused into its epilogue (kva_decode_gated -> d_attn_out), and the
+        O-projection (kva_out_project): with tp_size 1 into d_hidden with the
+        residual add (engine.py:2083-2085), else into d_proj_out without it
+        (engine.py:2086-2088, the all-reduce being the caller's).  The caller
+        advances current_len after the step, as decode_step does
+        (engine.py:1500)."""
+        kv = self._paged_kv("_decode_full_attention")
+        cfg = self.config
+        h = cfg.hidden_size
+        q_dim = self.local_num_attention_heads * cfg.head_dim
+        wq, wkv = self._stacked_weights(lw)
+        self._paged_step(layer_idx, 1, [kv.current_len], [position])
+        paged = kv.paged
+        layer = kv._full_layer_slot(layer_idx)
+        st = self._kva_stream
+        paged.project_append(layer, self.d_normed, h, wq, wkv, lw.q_norm, lw.k_norm, self.d_cos, self.d_sin,
+                             self.rope_rows, self.d_q, q_gate_out=self.d_q_gate,
+                             kv_out=getattr(self, "d_kv_fused", 0) or None, stream=st)
+        paged.decode(layer, self.d_q, self.d_attn_out, stream=st, gate=self.d_q_gate, gate_stride=q_dim)
+        if getattr(self, "tp_size", 1) <= 1:
+            paged.out_project(self.d_attn_out, 1, q_dim, lw.o_weight, h, self.d_hidden, residual=self.d_hidden,
+                              stream=st)
+        else:
+            paged.out_project(self.d_attn_out, 1, q_dim, lw.o_weight, h, self.d_proj_out, stream=st)
+
+    def _decode_full_attention_batched(self, layer_idx: int, lw, position: int, batch_size: int):
+        """Batched full-attention decode (engine.py:1778-1876): sequence b of
+        batch_size is KV batch slot b, appends its row at `position` and
+        attends over position + 1 rows, all in single launches instead of the
+        reference's per-sequence loop: kva_project_append over the batch's
+        rows of _d_normed_batch, kva_decode_gated, and kva_out_project of
+        every row into _d_proj_out_batch with the residual _d_hidden_batch
+        (engine.py:1872-1874).  Q, Q_gate and the attention output go to
+        contiguous [batch, q_dim] buffers of the launchers' own, allocated
+        once per batch size (the last one is also _d_attn_out_batch, the
+        name the reference gives it)."""
+        kv = self._paged_kv("_decode_full_attention_batched")
+        cfg = self.config
+        h = cfg.hidden_size
+        q_dim = self.local_num_attention_heads * cfg.head_dim
+        B = int(batch_size)
+        if not 1 <= B <= kv.batch_size:
+            raise ValueError(f"batch_size {B} outside the KVCache's {kv.batch_size} batch slots")
+        wq, wkv = self._stacked_weights(lw)
+        if getattr(self, "_kva_batch_bufs", (0,))[0] != B:
+            for p in getattr(self, "_kva_batch_bufs", (0,))[1:]:
+                self.device.free(p)
+            self._kva_batch_bufs = (B, *(self.device.malloc(B * q_dim * 2) for _ in range(3)))
+        _, d_q, d_gate, attn = self._kva_batch_bufs
+        self._d_attn_out_batch = attn
+        self._paged_step(layer_idx, 1, [int(position)] * B, [int(position)] * B)
+        paged = kv.paged
+        layer = kv._full_layer_slot(layer_idx)
+        st = self._kva_stream
+        paged.project_append(layer, self._d_normed_batch, h, wq, wkv, lw.q_norm, lw.k_norm, self.d_cos, self.d_sin,
+                             self.rope_rows, d_q, q_gate_out=d_gate, stream=st)
+        paged.decode(layer, d_q, attn, stream=st, gate=d_gate, gate_stride=q_dim)
+        paged.out_project(attn, B, q_dim, lw.o_weight, h, self._d_proj_out_batch, residual=self._d_hidden_batch,
+                          stream=st)
 
     # ---- decode launch cache (engine.py:3309-3555) ---------------------------
     def build_decode_launch_cache(self):
@@ -306,9 +387,10 @@ class FullAttentionLaunchers:
 ENGINE_METHODS = (
     "_launch_qknorm_rope", "_launch_qknorm_rope_cachew", "_launch_decode_attn_256",
     "_launch_decode_attn_256_gated", "_launch_decode_attn_256_batched", "_prefill_full_attention",
+    "_decode_full_attention", "_decode_full_attention_batched",
     "set_direct_kv_write", "build_decode_launch_cache", "rollback_kv_cache",
     # helpers the methods above call
-    "_rope_rows", "_workspace", "_stacked_weights", "_prefill_step",
+    "_rope_rows", "_workspace", "_stacked_weights", "_paged_kv", "_paged_step",
 )
 
 

@@ -158,9 +158,17 @@ class StubEngine:
                 lw.o_weight = device.array(wo).ptr
                 lw.q_norm, lw.k_norm, lw.attn_norm = device.array(qn).ptr, device.array(kn).ptr, device.array(an).ptr
             self.layers.append(lw)
-        self.d_q = device.malloc(q_dim * 2)
-        self.d_k = device.malloc(kv_dim * 2)
+        # The decode buffers of engine.py:1063-1077: [Q | Q_gate] and [K | V]
+        # contiguous, d_q / d_q_gate / d_k pointing into them.
+        self.d_q_fused = device.malloc(2 * q_dim * 2)
+        self.d_q, self.d_q_gate = self.d_q_fused, self.d_q_fused + q_dim * 2
+        self.d_kv_fused = device.malloc(2 * kv_dim * 2)
+        self.d_k = self.d_kv_fused
         self.d_attn_out = device.malloc(q_dim * 2)
+        self.d_normed = device.malloc(hidden * 2)
+        self.d_hidden = device.malloc(hidden * 2)
+        self.d_proj_out = device.malloc(hidden * 2)
+        self.tp_size = 1
 
     def _launch_rmsnorm(self, dst, src, weight, dim):
         x = np.frombuffer(self.device.download(src, dim * 2), np.float16).astype(np.float32)
@@ -173,7 +181,7 @@ class StubEngine:
         raise AssertionError("reference prefill called")
 
     _launch_qknorm_rope = _launch_decode_attn_256 = build_decode_launch_cache = rollback_kv_cache = \
-        _prefill_full_attention
+        _decode_full_attention = _decode_full_attention_batched = _prefill_full_attention
 
 
 def _ulp_close(got, exp, ulps=1):
@@ -242,6 +250,111 @@ def test_installed_prefill_full_attention(device):
             x_exp = orc.out_project(out_g.reshape(seq_len, q_dim), w["wo"], before)
             assert _ulp_close(rd(eng.d_pf_hidden, (seq_len, h)), x_exp), (seq_len, li)
         kv.current_len = start + seq_len  # prefill_step's bookkeeping (engine.py:3283)
+    kv.cleanup()
+
+
+def _fill_slot(device, kv, layer_idx, b, k, v):
+    """Rows [0, len(k)) of batch slot b: the KVCache's slot rows are
+    contiguous (consecutive pages), as in the reference layout."""
+    device.upload(kv.layer_k_ptr(layer_idx, b), k.tobytes())
+    device.upload(kv.layer_v_ptr(layer_idx, b), v.tobytes())
+
+
+def test_installed_decode_full_attention(device):
+    """_decode_full_attention (engine.py:1943-2092) on an installed engine:
+    two full-attention layers over a 40-row history, five decode steps at
+    positions current_len (the caller advancing current_len after each,
+    engine.py:1500).  Per layer and step, against the oracle chain
+    project_append -> attention_fp32 -> sigmoid_gate -> out_project: Q and
+    the appended K row within 4 ulps of each head row's largest element, Q_gate
+    and the V row within one ulp (the projection's rounding), the gated
+    attention within 2e-3 over every row so far, d_hidden within one ulp of
+    the O-projection plus the residual (engine.py:2083-2085)."""
+    from mi50grad_amd import attention as att
+    say("installed _decode_full_attention")
+    rng = np.random.default_rng(85)
+    cfg = AttnConfig(num_hidden_layers=8, hidden_size=512)
+    kv = KVCache(cfg, 128, device, batch_size=1)
+    eng = att.install(StubEngine(cfg, device, kv, rng, 512))
+    assert eng._decode_full_attention.__func__ is FullAttentionLaunchers._decode_full_attention
+    h, q_dim = 512, H * D
+    cos, sin = orc.rope_tables(128)
+    prefix = 40
+    for li in kv.full_layer_indices:
+        k0 = rng.standard_normal((prefix, HKV, D), dtype=np.float32).astype(np.float16)
+        v0 = rng.standard_normal((prefix, HKV, D), dtype=np.float32).astype(np.float16)
+        _fill_slot(device, kv, li, 0, k0, v0)
+    kv.current_len = prefix
+    rd = lambda p, shape: np.frombuffer(device.download(p, int(np.prod(shape)) * 2), np.float16).reshape(shape)
+    for step in range(5):
+        pos = kv.current_len
+        for li in kv.full_layer_indices:
+            w = eng.host[li]
+            normed = rng.standard_normal((1, h), dtype=np.float32).astype(np.float16)
+            before = rng.standard_normal((1, h), dtype=np.float32).astype(np.float16)
+            device.upload(eng.d_normed, normed.tobytes())
+            device.upload(eng.d_hidden, before.tobytes())
+            eng._decode_full_attention(li, eng.layers[li], pos)
+            device.synchronize()
+            q_o, g_o, _, k_o, v_o = orc.project_append(normed, w["wq"], w["wkv"], w["qn"], w["kn"], cos[[pos]],
+                                                       sin[[pos]])
+            q_g, g_g = rd(eng.d_q, (1, H, D)), rd(eng.d_q_gate, (1, H, D))
+            assert _row_close(q_g, q_o) and _ulp_close(g_g, g_o), (step, li)
+            ks, vs = kv.paged.gather(kv._full_layer_slot(li), 0, pos + 1)
+            assert _row_close(ks[pos:], k_o) and _ulp_close(vs[pos:], v_o), (step, li)
+            out_g = rd(eng.d_attn_out, (1, H, D))
+            exp = orc.sigmoid_gate(orc.attention_fp32(q_g, ks, vs).astype(np.float16), g_g)
+            assert max_err(out_g, exp) <= 2e-3, (step, li)
+            x_exp = orc.out_project(out_g.reshape(1, q_dim), w["wo"], before)
+            assert _ulp_close(rd(eng.d_hidden, (1, h)), x_exp), (step, li)
+        kv.advance()
+    kv.cleanup()
+
+
+def test_installed_decode_full_attention_batched(device):
+    """_decode_full_attention_batched (engine.py:1778-1876): three batch
+    slots with their own 37-row histories append at position 37 and attend
+    over 38 rows, two steps, each stage against the oracle as above, the
+    O-projection of every row into _d_proj_out_batch with the residual
+    _d_hidden_batch (engine.py:1872-1874)."""
+    from mi50grad_amd import attention as att
+    say("installed _decode_full_attention_batched")
+    rng = np.random.default_rng(86)
+    cfg = AttnConfig(num_hidden_layers=4, hidden_size=512)
+    B, P, h, q_dim = 3, 37, 512, H * D
+    kv = KVCache(cfg, 64, device, batch_size=4)
+    eng = att.install(StubEngine(cfg, device, kv, rng, 512))
+    eng._d_normed_batch = device.malloc(B * h * 2)
+    eng._d_hidden_batch = device.malloc(B * h * 2)
+    eng._d_proj_out_batch = device.malloc(B * h * 2)
+    cos, sin = orc.rope_tables(64)
+    li = kv.full_layer_indices[0]
+    w = eng.host[li]
+    for b in range(B):
+        _fill_slot(device, kv, li, b, rng.standard_normal((P, HKV, D), dtype=np.float32).astype(np.float16),
+                   rng.standard_normal((P, HKV, D), dtype=np.float32).astype(np.float16))
+    rd = lambda p, shape: np.frombuffer(device.download(p, int(np.prod(shape)) * 2), np.float16).reshape(shape)
+    for position in (P, P + 1):
+        normed = rng.standard_normal((B, h), dtype=np.float32).astype(np.float16)
+        hid = rng.standard_normal((B, h), dtype=np.float32).astype(np.float16)
+        device.upload(eng._d_normed_batch, normed.tobytes())
+        device.upload(eng._d_hidden_batch, hid.tobytes())
+        eng._decode_full_attention_batched(li, eng.layers[li], position, B)
+        device.synchronize()
+        pos = [position] * B
+        q_o, g_o, _, k_o, v_o = orc.project_append(normed, w["wq"], w["wkv"], w["qn"], w["kn"], cos[pos], sin[pos])
+        _, d_q, d_gate, d_attn = eng._kva_batch_bufs
+        q_g, g_g = rd(d_q, (B, H, D)), rd(d_gate, (B, H, D))
+        assert _row_close(q_g, q_o) and _ulp_close(g_g, g_o), position
+        out_g = rd(d_attn, (B, H, D))
+        for b in range(B):
+            ks, vs = kv.paged.gather(kv._full_layer_slot(li), b, position + 1)
+            assert _row_close(ks[position:], k_o[b:b + 1]) and _ulp_close(vs[position:], v_o[b:b + 1]), (position, b)
+            exp = orc.sigmoid_gate(orc.attention_fp32(q_g[b:b + 1], ks, vs).astype(np.float16), g_g[b:b + 1])
+            assert max_err(out_g[b:b + 1], exp) <= 2e-3, (position, b)
+        x_exp = orc.out_project(out_g.reshape(B, q_dim), w["wo"], hid)
+        assert _ulp_close(rd(eng._d_proj_out_batch, (B, h)), x_exp), position
+        assert np.array_equal(rd(eng._d_hidden_batch, (B, h)).view(np.uint16), hid.view(np.uint16))
     kv.cleanup()
 
 
