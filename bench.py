@@ -746,6 +746,38 @@ def copy_probe(dev, gib: float = 4.0, reps: int = 20):
     return {"bytes_per_launch": 2 * n, "avg_us": ms * 1e3, "gbs": 2 * n / (ms * 1e-3) / 1e9}
 
 
+def page_read_probe(dev, reps: int = 20, copies: int = 4):
+    """The read ceiling of the decode's own access pattern: kva_hbm_read_pages
+    over config 3's pages (the same lengths, the same permuted page ids, 256
+    workgroups of four waves), rotating over `copies` layers' pools so no
+    launch finds the previous one's pages in the MALL; average of `reps`
+    launches between HIP events."""
+    spec = wl.c3_spec(0)
+    ids = np.concatenate([np.asarray(b[:(int(L) + 1 + 15) // 16], np.int32)
+                          for L, b in zip(spec.lengths, spec.block_ids)])
+    cache = PagedKVCache(n_layers=copies, max_seqs=1, max_blocks=spec.n_blocks, max_blocks_per_seq=1,
+                         max_step_tokens=16)
+    d_ids, sink = dev.array(ids), dev.malloc(256)
+    pools = [cache.layer_pools(i) for i in range(copies)]
+    n_cu = device_props()["n_cu"]
+    call = lambda i: _lib.call("kva_hbm_read_pages", pools[i % copies][0], pools[i % copies][1], d_ids.ptr,
+                               len(ids), HKV, n_cu, sink, None)
+    for i in range(copies):
+        call(i)
+    s, e = Event(), Event()
+    s.record()
+    for i in range(reps):
+        call(i)
+    e.record()
+    e.synchronize()
+    ms = s.elapsed_ms(e) / reps
+    by = len(ids) * 16 * ROW_BYTES  # K and V of every row of every page
+    dev.free(sink)
+    d_ids.free()
+    cache.destroy()
+    return {"bytes_per_launch": by, "avg_us": ms * 1e3, "gbs": by / (ms * 1e-3) / 1e9, "pages": len(ids)}
+
+
 def read_probe(dev, gib: float = 4.0, reps: int = 20):
     """The HBM read ceiling: kva_hbm_read over `gib` GiB, average of `reps`
     launches between HIP events."""
@@ -886,9 +918,10 @@ def load_traffic(name: str):
 
 def workload_line(dev, args) -> dict:
     """The bench line (a dict) of every workload but the decode ones."""
-    if args.workload in ("copy", "read"):
-        r = copy_probe(dev) if args.workload == "copy" else read_probe(dev)
-        return ({"metric": f"HBM stream {args.workload} GB/s", "value": r["gbs"], "unit": "GB/s",
+    if args.workload in ("copy", "read", "pages"):
+        r = {"copy": copy_probe, "read": read_probe, "pages": page_read_probe}[args.workload](dev)
+        return ({"metric": f"HBM {'paged' if args.workload == 'pages' else 'stream'} read GB/s"
+                 if args.workload != "copy" else "HBM stream copy GB/s", "value": r["gbs"], "unit": "GB/s",
                           "n_gpus": 1, "avg_us": r["avg_us"], "bytes_per_launch": r["bytes_per_launch"],
                           "higher_is_better": True})
     if args.workload == "c1":
@@ -1015,7 +1048,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "proj4", "copy", "read"])
+    ap.add_argument("--workload", default="c3", choices=["c1", "c3", "ctx8192", "c2", "c2graph", "c4", "c5", "proj", "proj4", "copy", "read", "pages"])
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
@@ -1042,14 +1075,19 @@ def main() -> int:
         line["ctx8192"]["config"] = sub["config"]["workload"]
         line["ctx8192"]["roofline"] = {k: sub["roofline"][k] for k in ("achieved", "frac", "avg_us",
                                                                          "alg_bytes_per_launch", "decode_kernel")}
-        rd, cp = read_probe(dev), copy_probe(dev)
+        rd, cp, pr = read_probe(dev), copy_probe(dev), page_read_probe(dev)
+        dk = line["roofline"]["decode_kernel"]["achieved"]
         line["peaks"] = {
             "vendor_hbm_gbs": HBM_PEAK_GBS,
+            "measured_page_read_gbs": pr["gbs"],
             "measured_stream_read_gbs": rd["gbs"], "measured_stream_copy_gbs": cp["gbs"],
-            "decode_frac_of_measured_read": line["roofline"]["achieved"] / rd["gbs"],
-            "method": "kva_hbm_read over 4 GiB (read-only: 2048 contiguous shares, two passes of 4 x 16-byte loads per lane in flight) and "
-                      "kva_hbm_copy over 4 GiB (bytes read + written), averages of 20 launches between "
-                      "HIP events; roofline.frac stays against the vendor 8 TB/s"}
+            "decode_kernel_frac_of_page_read": dk / pr["gbs"],
+            "decode_call_frac_of_page_read": line["roofline"]["achieved"] / pr["gbs"],
+            "method": "kva_hbm_read_pages over config 3's permuted pages (the decode kernel's own per-wave loads, "
+                      "no arithmetic, 256 workgroups, four pools rotated); kva_hbm_read over 4 GiB (read-only: "
+                      "2048 contiguous shares, two passes of 4 x 16-byte loads per lane in flight) and "
+                      "kva_hbm_copy over 4 GiB (bytes read + written); averages of 20 launches between HIP "
+                      "events; roofline.frac stays against the vendor 8 TB/s"}
     if args.workload == "c3" and not args.no_extras:
         line["other_configs"] = other_configs(dev, args)
     if not args.no_cpu_baseline:

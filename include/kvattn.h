@@ -417,6 +417,18 @@ int kva_hbm_copy(void *dst, const void *src, size_t bytes, kva_stream_t stream);
  * counterpart of the reference's bench/micro/hbm_bandwidth.hip.cpp.        */
 int kva_hbm_read(const void *src, size_t bytes, void *sink, kva_stream_t stream);
 
+/* Paged HBM read probe: the stream-K decode's own load pattern with no
+ * arithmetic.  n_wg workgroups of num_kv_heads waves share the page list
+ * page_ids[0 .. n_pages) (a DEVICE int32 array) in equal contiguous ranges;
+ * wave h reads kv head h's 512-byte slice of every row of each page of K and
+ * of V (pools [page][16][num_kv_heads][256] fp16), as decode_mfma_kernel
+ * does, one page in flight while the previous is folded by XOR; `sink` (one
+ * 4-byte word) is written only when the fold hits a fixed value.  The read
+ * ceiling of the decode's access pattern, next to kva_hbm_read's contiguous
+ * stream (bench/micro/hbm_bandwidth.hip.cpp is the reference's probe).     */
+int kva_hbm_read_pages(const void *k_pool, const void *v_pool, const int32_t *page_ids, int32_t n_pages,
+                       int32_t num_kv_heads, int32_t n_wg, void *sink, kva_stream_t stream);
+
 /* ---- device helpers (the GPUDevice surface, hip_dispatch.py:594-703) ----- */
 int kva_dev_count(int32_t *n);
 /* The current device's compute units, peak shader clock (kHz), memory clock

@@ -81,6 +81,7 @@ SIGNATURES = {
     "kva_set_decode_split": [_P, _I],
     "kva_get_decode_split": [_P, _PI, _PI],
     "kva_kernel_events": [_P, _P, _P],
+    "kva_hbm_read_pages": [_P, _P, _P, _I, _I, _I, _P, _P],
     "kva_timeline_enable": [_P, _I],
     "kva_get_project_path": [_P, _PI],
     "kva_timeline_read": [_P, POINTER(c_uint64), c_size_t, _PI, _PI],

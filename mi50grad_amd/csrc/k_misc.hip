@@ -93,7 +93,74 @@ __global__ __launch_bounds__(256) void read_kernel(const uint4 *__restrict__ src
     if (acc == magic) sink[0] = acc;
 }
 
+// Paged read probe: the stream-K decode's loads without its arithmetic.
+// Workgroup w of gridDim.x takes the pages [w*P/W, (w+1)*P/W) of the list;
+// wave h (one per kv head) reads head h's 512-byte slice of every row of
+// each page exactly as decode_mfma_kernel does (K: lane l reads 128
+// contiguous bytes of row l%16 at byte 128*(l/16); V: 8 bytes at 8*l of every
+// row), one page in flight while the previous one is folded.  Page ids are
+// scalar loads, as in the decode.
+__device__ __forceinline__ void fold_page(uint32_t &acc, const uint4 (&k)[8], const uint2 (&v)[kBlockTokens]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc ^= fold16(k[i]);
+#pragma unroll
+    for (int t = 0; t < kBlockTokens; ++t) acc ^= v[t].x ^ v[t].y;
+}
+
+__global__ __launch_bounds__(256) void page_read_kernel(const uint8_t *k_pool, const uint8_t *v_pool,
+                                                        const int32_t *page_ids, int32_t n_pages, int32_t row_bytes,
+                                                        uint32_t *sink, uint32_t magic) {
+    const int w = blockIdx.x, W = gridDim.x;
+    const int p0 = static_cast<int>(static_cast<int64_t>(w) * n_pages / W);
+    const int p1 = static_cast<int>(static_cast<int64_t>(w + 1) * n_pages / W);
+    const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
+    const uint32_t koff = (lane & 15) * row_bytes + 128 * (lane >> 4);
+    const uint32_t voff = 8 * lane;
+    auto load = [&](uint4 (&k)[8], uint2 (&v)[kBlockTokens], int p) {
+        const bool on = p < p1;
+        const int id = on ? ld_uniform(page_ids + p) : 0;
+        const size_t ofs = static_cast<size_t>(id) * page_bytes + h * kHeadDim * 2;
+        const auto rk = ro_rsrc(k_pool + ofs, on ? page_bytes : 0u);
+        const auto rv = ro_rsrc(v_pool + ofs, on ? page_bytes : 0u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * i, 0, 0);
+            k[i] = make_uint4(x[0], x[1], x[2], x[3]);
+        }
+#pragma unroll
+        for (int t = 0; t < kBlockTokens; ++t) {
+            const auto x = __builtin_amdgcn_raw_buffer_load_b64(rv, voff + t * row_bytes, 0, 0);
+            v[t] = make_uint2(x[0], x[1]);
+        }
+    };
+    uint32_t acc = 0;
+    uint4 ka[8], kb[8];
+    uint2 va[kBlockTokens], vb[kBlockTokens];
+    int p = p0;
+    load(ka, va, p);
+    while (p < p1) {
+        load(kb, vb, p + 1);
+        fold_page(acc, ka, va);
+        if (++p >= p1) break;
+        load(ka, va, p + 1);
+        fold_page(acc, kb, vb);
+        ++p;
+    }
+    if (acc == magic) sink[0] = acc;
+}
+
 }  // namespace
+
+hipError_t launch_read_pages(const void *k_pool, const void *v_pool, const int32_t *page_ids, int32_t n_pages,
+                             int32_t num_kv_heads, int32_t n_wg, uint32_t *sink, hipStream_t s) {
+    if (n_pages <= 0) return hipSuccess;
+    hipLaunchKernelGGL(page_read_kernel, dim3(n_wg), dim3(64 * num_kv_heads), 0, s,
+                       static_cast<const uint8_t *>(k_pool), static_cast<const uint8_t *>(v_pool), page_ids, n_pages,
+                       num_kv_heads * kHeadDim * 2, sink, 0x9e3779b9u);
+    return hipGetLastError();
+}
 
 hipError_t launch_read(const void *src, size_t bytes, uint32_t *sink, hipStream_t s) {
     const size_t n16 = bytes / 16;

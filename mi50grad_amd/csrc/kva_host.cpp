@@ -1739,6 +1739,21 @@ int kva_hbm_read(const void *src, size_t bytes, void *sink, kva_stream_t stream)
     return KVA_OK;
 }
 
+int kva_hbm_read_pages(const void *k_pool, const void *v_pool, const int32_t *page_ids, int32_t n_pages,
+                       int32_t num_kv_heads, int32_t n_wg, void *sink, kva_stream_t stream) {
+    if (!k_pool || !v_pool || !page_ids || !sink) return fail(KVA_ERR_INVALID_ARG, "NULL pointer");
+    if (n_pages < 0) return fail(KVA_ERR_INVALID_ARG, "n_pages %d < 0", n_pages);
+    if (num_kv_heads < 1 || num_kv_heads > 16)
+        return fail(KVA_ERR_UNSUPPORTED, "num_kv_heads %d outside [1, 16]", num_kv_heads);
+    if (n_wg < 1 || n_wg > 65535) return fail(KVA_ERR_INVALID_ARG, "n_wg %d outside [1, 65535]", n_wg);
+    if (!aligned16(k_pool) || !aligned16(v_pool) || (reinterpret_cast<uintptr_t>(page_ids) & 3u) ||
+        (reinterpret_cast<uintptr_t>(sink) & 3u))
+        return fail(KVA_ERR_MISALIGNED, "pools must be 16-byte, page ids and sink 4-byte aligned");
+    KVA_HIP(kva::launch_read_pages(k_pool, v_pool, page_ids, n_pages, num_kv_heads, n_wg, static_cast<uint32_t *>(sink),
+                                   static_cast<hipStream_t>(stream)));
+    return KVA_OK;
+}
+
 // ---- device helpers -------------------------------------------------------
 int kva_dev_count(int32_t *n) {
     if (!n) return fail(KVA_ERR_INVALID_ARG, "NULL argument");

@@ -190,6 +190,11 @@ hipError_t launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 // Read-only stream over `bytes` (multiple of 16): the read-bandwidth probe.
 // sink: one word, written only when the data's XOR fold hits a fixed value.
 hipError_t launch_read(const void *src, size_t bytes, uint32_t *sink, hipStream_t s);
+// Paged read probe: the pages page_ids[0 .. n_pages) (device array) of the
+// K and V pools, [page][16][num_kv_heads][256] fp16, read with the stream-K
+// decode's per-wave pattern by n_wg workgroups of one wave per kv head.
+hipError_t launch_read_pages(const void *k_pool, const void *v_pool, const int32_t *page_ids, int32_t n_pages,
+                             int32_t num_kv_heads, int32_t n_wg, uint32_t *sink, hipStream_t s);
 
 // Move accepted rows of each sequence, in every layer (tree rollback).
 struct RollbackArgs {

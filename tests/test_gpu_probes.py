@@ -39,3 +39,28 @@ def test_copy_and_read_probes():
         _lib.call("kva_hbm_read", z.ptr, 20, sink.ptr, None)
     for x in (a, b, sink, z, one):
         x.free()
+
+
+def test_paged_read_probe():
+    """kva_hbm_read_pages reads exactly the listed pages with the decode's
+    per-wave pattern: zero pages leave the sink alone; a listed page holding
+    the magic 16 bytes at K row 0, head 0 (lane 0 of wave 0's first load)
+    writes it, the same page left off the list does not."""
+    dev = GPUDevice(0)
+    say("paged read probe")
+    pages, hkv = 4, 4
+    page_words = 16 * hkv * 256 // 2  # uint32 words of one page (fp16 rows)
+    k = np.zeros(pages * page_words, np.uint32)
+    k[2 * page_words] = 0x9E3779B9
+    dk, dv = dev.array(k), dev.array(np.zeros_like(k))
+    sink = dev.array(np.full(4, 7, np.uint32))
+    for ids, hit in (([3, 0], False), ([3, 2, 0], True)):
+        sink.copy_from(np.full(4, 7, np.uint32))
+        d_ids = dev.array(np.asarray(ids, np.int32))
+        for n_wg in (1, 2):
+            _lib.call("kva_hbm_read_pages", dk.ptr, dv.ptr, d_ids.ptr, len(ids), hkv, n_wg, sink.ptr, None)
+        dev.synchronize()
+        assert sink.numpy().tolist() == ([0x9E3779B9, 7, 7, 7] if hit else [7, 7, 7, 7]), ids
+        d_ids.free()
+    for x in (dk, dv, sink):
+        x.free()

@@ -346,3 +346,13 @@ def test_legacy_decode_without_workspace_refuses_long_caches():
     with pytest.raises(KvaError, match="workspace") as e:
         _lib.call("kva_legacy_decode_batched", None, FAKE, FAKE, FAKE, FAKE, 5000, 2, 5000 * 2048, 24, 4, None)
     assert code(e) == -8
+
+
+def test_paged_read_probe_refusals():
+    """kva_hbm_read_pages validates before any launch (fake pointers)."""
+    for args, want in (((FAKE, FAKE, FAKE, 4, 4, 0, FAKE), -1), ((FAKE, FAKE, FAKE, -1, 4, 8, FAKE), -1),
+                       ((FAKE, FAKE, FAKE, 4, 17, 8, FAKE), -2), ((FAKE + 8, FAKE, FAKE, 4, 4, 8, FAKE), -10),
+                       ((None, FAKE, FAKE, 4, 4, 8, FAKE), -1)):
+        with pytest.raises(KvaError) as e:
+            _lib.call("kva_hbm_read_pages", *args, None)
+        assert code(e) == want, args
