@@ -29,7 +29,8 @@ sequence at 8192 rows), c2
 same with the 16-layer step recorded once and replayed), c4 (chunked
 prefill), c5 (tree verify + rollback), proj (config 3 with its producer:
 the fused Q/K/V projection + append, then the gated decode), proj4 (the
-config-4 producer: 2048 tokens through the library GEMM), copy and read
+config-4 producer: 2048 tokens through the tiled prefill GEMM with the
+QK-norm/RoPE/append epilogue fused in), copy and read
 (HBM stream probes: the measured bandwidth ceilings).
 """
 from __future__ import annotations

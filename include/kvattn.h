@@ -19,12 +19,8 @@
  *     so two calls on one cache that overlap on different streams race:
  *     use one stream per cache, or one cache per stream;
  *   - the library allocates device memory in kva_create and the kva_dev_*
- *     helpers, plus two named exceptions: the first prefill-sized
- *     kva_project_append on a cache (more than 64 tokens, outside a
- *     recording) sets up its library GEMM once (a 2048-token fp16 output
- *     and a 64 MB workspace), and kva_timeline_enable allocates the
- *     timeline buffer.  No other call allocates; kva_legacy_decode_noalloc
- *     allocates nothing at all;
+ *     helpers, and in kva_timeline_enable (the timeline buffer).  No other
+ *     call allocates; kva_legacy_decode_noalloc allocates nothing at all;
  *   - every call validates its arguments before it touches the device, so a
  *     host-only cache (KVA_FLAG_HOST_ONLY) reports the same refusals and
  *     answers a call that would pass them with KVA_ERR_NO_DEVICE.
@@ -189,17 +185,15 @@ int kva_project_append(kva_cache *cache, int32_t layer, const void *x, int32_t h
                        const void *cos_tab, const void *sin_tab, int32_t table_rows,
                        void *q_out, void *q_gate_out, void *kv_out, kva_stream_t stream);
 /* How the last kva_project_append on this cache projected: steps of up to
- * 64 tokens through libkvattn's projection kernels (the weights are read
- * once per 64 tokens); larger steps through one hipBLASLt GEMM per weight
- * matrix over up to 2048 tokens (the reference's batched prefill GEMMs,
- * engine.py:3051-3068) that round the fp32 sums to fp16 on output, then
- * the same finish kernel (norm, RoPE, append).  A larger step goes through the projection kernels when
- * the GEMM cannot be set up (first call while a graph is being recorded,
- * no device memory for its 64 MB workspace and 2048-token output, or no
- * library solution for the shape): the results satisfy the same contract
- * either way; this says which ran.                                         */
+ * 64 tokens through the split-K projection kernels and their finish kernel
+ * (the weights are read once per 64 tokens); larger steps through one
+ * prefill GEMM launch (the reference's batched prefill GEMM,
+ * gemm_fp16_prefill.hip:47 at engine.py:3051-3068) whose tiles of 128
+ * tokens x one head's 256 weight rows each finish their own rows: fp32 sums
+ * rounded to fp16, then the same norm, RoPE and append.  The results
+ * satisfy the same contract either way; this says which ran.               */
 #define KVA_PROJECT_KERNELS 0
-#define KVA_PROJECT_LIBRARY_GEMM 1
+#define KVA_PROJECT_PREFILL_GEMM 1
 int kva_get_project_path(const kva_cache *cache, int32_t *path);
 /* Output projection of the (gated) attention rows, the consumer of
  * kva_decode_gated: out[t] = fp16(attn[t] . W_o^T + residual[t]) for

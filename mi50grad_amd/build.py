@@ -60,7 +60,7 @@ def build(verbose: bool = False) -> Path:
     objs = sorted(str(p) for p in objdir.glob("*.o"))
     tmp = OUT.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs,
-          f"-L{ROCM / 'lib'}", "-lamdhip64", "-lhipblaslt", f"-Wl,-rpath,{ROCM / 'lib'}"])
+          f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"])
     os.replace(tmp, OUT)
     shutil.rmtree(objdir)
     return OUT

@@ -313,14 +313,11 @@ __global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
     const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
     const NormRopeIn nin = norm_rope_in<32>(hr < H ? a.q_w : a.k_w, cos_row, sin_row, a.half_rot, lane);
     // Every split's partial is loaded at once (splits past a.splits reread
-    // split 0 and are not added), then summed in split order; or the
-    // projection as the library GEMM rounded it.
+    // split 0 and are not added), then summed in split order.
     const size_t N = static_cast<size_t>(a.n_a) + a.n_b;
     const size_t row_at = static_cast<size_t>(tc) * N + static_cast<size_t>(hr) * kHeadDim + 8 * lane;
     uint4 y;
-    if (a.part16) {
-        y = ld16(a.part16 + row_at);
-    } else {
+    {
         const size_t split_stride = static_cast<size_t>(a.n_tok) * N;
         const float *p = a.part + row_at;
         float4_t plo[kProjMaxSplits], phi[kProjMaxSplits];
@@ -446,13 +443,6 @@ hipError_t launch_project(const ProjectArgs &a, hipStream_t s) {
     if (a.n_tok <= 0) return hipSuccess;
     const hipError_t e = launch_proj_gemm_timed(a, s);
     if (e != hipSuccess) return e;
-    const int blocks_per_tok = (2 * a.num_heads + 2 * a.num_kv_heads + 7) / 8;
-    hipLaunchKernelGGL(proj_finish_kernel, dim3(a.n_tok * blocks_per_tok), dim3(256), 0, s, a);
-    return hipGetLastError();
-}
-
-hipError_t launch_project_finish(const ProjectArgs &a, hipStream_t s) {
-    if (a.n_tok <= 0) return hipSuccess;
     const int blocks_per_tok = (2 * a.num_heads + 2 * a.num_kv_heads + 7) / 8;
     hipLaunchKernelGGL(proj_finish_kernel, dim3(a.n_tok * blocks_per_tok), dim3(256), 0, s, a);
     return hipGetLastError();

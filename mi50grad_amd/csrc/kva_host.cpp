@@ -14,8 +14,6 @@
 #include "../../include/kvattn.h"
 #include "kva_internal.h"
 
-#include <hipblaslt/hipblaslt.h>
-
 #include <algorithm>
 #include <cstdarg>
 #include <cstdint>
@@ -87,25 +85,7 @@ struct kva_cache {
     int32_t mq_max_wg = 0;
     float *d_proj = nullptr;    // projection partials [kProjMaxSplits][kProjTokens][(2H+2Hkv)*256]
     size_t proj_floats = 0;
-    // Prefill-sized projections (steps of more than kProjTokens tokens): one
-    // library GEMM per weight matrix over up to big_tokens tokens into
-    // d_proj_big [big_tokens][(2H+2Hkv)*256] fp16, then the finish kernel.
-    // Set up on the first such call.
-    uint16_t *d_proj_big = nullptr;
-    int32_t big_tokens = 0;
-    hipblasLtHandle_t lt = nullptr;
-    void *lt_ws = nullptr;
-    bool lt_tried = false;       // set-up attempted (it is not retried)
-    struct LtPlan {
-        int64_t T, N, K, ldd;
-        hipblasLtMatmulDesc_t op;
-        hipblasLtMatrixLayout_t la, lb, lc;
-        hipblasLtMatmulAlgo_t algo;
-        size_t ws;
-        bool ok;
-    };
-    std::vector<LtPlan> lt_plans;
-    int32_t last_proj_path = 0;  // KVA_PROJECT_KERNELS or KVA_PROJECT_LIBRARY_GEMM
+    int32_t last_proj_path = 0;  // KVA_PROJECT_KERNELS or KVA_PROJECT_PREFILL_GEMM
     int32_t max_wg = 0;  // decode workgroups the partial workspace can serve
     size_t ws_rows = 0;  // 256-float rows in the decode partial workspace
     int32_t n_cu = 0;
@@ -453,15 +433,6 @@ int kva_destroy(kva_cache *c) {
         (void)hipFree(c->d_ws_acc);
         (void)hipFree(c->d_ws_ml);
         (void)hipFree(c->d_timeline);
-        for (auto &pl : c->lt_plans) {
-            if (pl.lc) (void)hipblasLtMatrixLayoutDestroy(pl.lc);
-            if (pl.lb) (void)hipblasLtMatrixLayoutDestroy(pl.lb);
-            if (pl.la) (void)hipblasLtMatrixLayoutDestroy(pl.la);
-            if (pl.op) (void)hipblasLtMatmulDescDestroy(pl.op);
-        }
-        if (c->lt) (void)hipblasLtDestroy(c->lt);
-        (void)hipFree(c->lt_ws);
-        (void)hipFree(c->d_proj_big);
         (void)hipFree(c->d_mq_acc);
         (void)hipFree(c->d_mq_ml);
         (void)hipFree(c->d_proj);
@@ -866,74 +837,6 @@ static int32_t project_splits(const kva_cache *c, int32_t hidden, int32_t n_rows
     return best;
 }
 
-// Tokens of one library GEMM of a prefill-sized projection (its output, fp16
-// rounded from fp32 sums, is [tokens][(2H+2Hkv)*256], 59 MB at 2048 tokens
-// and 24 + 4 heads), and the GEMM's workspace.
-constexpr int32_t kBigProjTokens = 2048;
-constexpr size_t kLtWorkspaceBytes = size_t(64) << 20;
-
-// Set up the library GEMM once per cache (outside a recording: it
-// allocates).  Returns false when it cannot be used; the step then goes
-// through the projection kernels 64 tokens at a time.
-static bool big_project_ready(kva_cache *c) {
-    if (c->lt) return true;
-    if (c->lt_tried || c->capturing) return false;
-    c->lt_tried = true;
-    const int32_t tokens = std::min(c->cfg.max_step_tokens, kBigProjTokens);
-    const size_t n = 2 * static_cast<size_t>(c->cfg.num_heads + c->cfg.num_kv_heads) * kva::kHeadDim;
-    if (hipMalloc(&c->d_proj_big, static_cast<size_t>(tokens) * n * sizeof(uint16_t)) != hipSuccess ||
-        hipMalloc(&c->lt_ws, kLtWorkspaceBytes) != hipSuccess || hipblasLtCreate(&c->lt) != HIPBLAS_STATUS_SUCCESS) {
-        (void)hipGetLastError();
-        (void)hipFree(c->d_proj_big);
-        (void)hipFree(c->lt_ws);
-        c->d_proj_big = nullptr;
-        c->lt_ws = nullptr;
-        c->lt = nullptr;
-        return false;
-    }
-    c->big_tokens = tokens;
-    return true;
-}
-
-// The plan of D[T][ldd] (fp16 from fp32 sums, N columns) = X[T][K] (fp16) .
-// W[N][K]^T (fp16): in the library's column-major terms D^T (N x T, ld ldd)
-// = op(A) B with A = W stored K x N (ld K) transposed and B = X stored K x T
-// (ld K).  The fp16 output is the projection the reference's GEMV stores.
-static kva_cache::LtPlan *lt_plan(kva_cache *c, int64_t T, int64_t N, int64_t K, int64_t ldd) {
-    for (auto &pl : c->lt_plans)
-        if (pl.T == T && pl.N == N && pl.K == K && pl.ldd == ldd) return &pl;
-    kva_cache::LtPlan pl{};
-    pl.T = T;
-    pl.N = N;
-    pl.K = K;
-    pl.ldd = ldd;
-    pl.ok = false;
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    hipblasLtMatmulPreference_t pref = nullptr;
-    const uint64_t ws_max = kLtWorkspaceBytes;
-    hipblasLtMatmulHeuristicResult_t res{};
-    int found = 0;
-    if (hipblasLtMatmulDescCreate(&pl.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulDescSetAttribute(pl.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulDescSetAttribute(pl.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&pl.la, HIP_R_16F, K, N, K) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&pl.lb, HIP_R_16F, K, T, K) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&pl.lc, HIP_R_16F, N, T, ldd) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws_max,
-                                              sizeof(ws_max)) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulAlgoGetHeuristic(c->lt, pl.op, pl.la, pl.lb, pl.lc, pl.lc, pref, 1, &res, &found) ==
-            HIPBLAS_STATUS_SUCCESS &&
-        found > 0 && res.state == HIPBLAS_STATUS_SUCCESS && res.workspaceSize <= kLtWorkspaceBytes) {
-        pl.algo = res.algo;
-        pl.ws = res.workspaceSize;
-        pl.ok = true;
-    }
-    if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
-    c->lt_plans.push_back(pl);
-    return &c->lt_plans.back();
-}
-
 static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidden, const void *w_q_fused,
                         const void *w_kv_fused, const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
                         const void *sin_tab, int32_t table_rows, void *q_out, void *q_gate_out, void *kv_out,
@@ -990,43 +893,17 @@ static int project_impl(kva_cache *c, int32_t layer, const void *x, int32_t hidd
     a.ev_after = c->kev_after;
     const auto *xs = static_cast<const uint16_t *>(x);
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    // Prefill-sized steps: the weights are read once per kBigProjTokens
-    // tokens by a library GEMM (the reference's batched path at seq_len >= 32,
-    // engine.py:3051-3068), not once per 64 tokens.  Every plan is made (and
-    // checked) before anything is launched.
-    if (c->st_n_tok > kva::kProjTokens && !c->capturing && big_project_ready(c)) {
-        const int64_t N = static_cast<int64_t>(a.n_a) + a.n_b;
-        bool ok = true;
-        for (int32_t t0 = 0; t0 < c->st_n_tok && ok; t0 += c->big_tokens) {
-            const int64_t n = std::min(c->big_tokens, c->st_n_tok - t0);
-            ok = lt_plan(c, n, a.n_a, hidden, N)->ok && lt_plan(c, n, a.n_b, hidden, N)->ok;
-        }
-        if (ok) {
-            const float one = 1.0f, zero = 0.0f;
-            a.splits = 1;
-            a.part16 = c->d_proj_big;
-            for (int32_t t0 = 0; t0 < c->st_n_tok; t0 += c->big_tokens) {
-                const int32_t n = std::min(c->big_tokens, c->st_n_tok - t0);
-                const uint16_t *xc = xs + static_cast<size_t>(t0) * hidden;
-                if (c->kev_before) KVA_HIP(hipEventRecord(c->kev_before, s));
-                for (int m = 0; m < 2; ++m) {
-                    const kva_cache::LtPlan *pl = lt_plan(c, n, m ? a.n_b : a.n_a, hidden, N);
-                    uint16_t *d = c->d_proj_big + (m ? a.n_a : 0);
-                    const hipblasStatus_t st =
-                        hipblasLtMatmul(c->lt, pl->op, &one, m ? a.w_b : a.w_a, pl->la, xc, pl->lb, &zero, d, pl->lc, d,
-                                        pl->lc, &pl->algo, c->lt_ws, pl->ws, s);
-                    if (st != HIPBLAS_STATUS_SUCCESS)
-                        return fail(KVA_ERR_INVALID_ARG, "hipblasLtMatmul failed (status %d)", static_cast<int>(st));
-                }
-                if (c->kev_after) KVA_HIP(hipEventRecord(c->kev_after, s));
-                a.tok0 = t0;
-                a.n_tok = n;
-                a.x = xc;
-                KVA_HIP(kva::launch_project_finish(a, s));
-            }
-            c->last_proj_path = KVA_PROJECT_LIBRARY_GEMM;
-            return KVA_OK;
-        }
+    // Prefill-sized steps: one GEMM launch whose tiles are whole heads, the
+    // epilogue fused (the reference's batched path at seq_len >= 32,
+    // engine.py:3051-3068), instead of 64-token launch pairs that would
+    // each read all the weights.
+    if (c->st_n_tok > kva::kProjTokens) {
+        a.tok0 = 0;
+        a.n_tok = c->st_n_tok;
+        a.x = xs;
+        KVA_HIP(kva::launch_project_big(a, s));
+        c->last_proj_path = KVA_PROJECT_PREFILL_GEMM;
+        return KVA_OK;
     }
     for (int32_t t0 = 0; t0 < c->st_n_tok; t0 += kva::kProjTokens) {
         a.tok0 = t0;

@@ -69,8 +69,6 @@ struct ProjectArgs {
     int32_t n_tok;            // tokens of this chunk, 1..kProjTokens
     int32_t splits;
     float *part;              // [splits][n_tok][n_a + n_b]
-    const uint16_t *part16;   // or the projection already rounded to fp16,
-                              // [n_tok][n_a + n_b] (the library GEMM's output)
     int32_t tok0;             // the chunk's first token within the step
     uint16_t *q_out;          // [T][H][256]: normalised + rotated Q
     uint16_t *gate_out;       // [T][H][256]: Q_gate as projected (nullable)
@@ -99,10 +97,15 @@ struct ProjectArgs {
     hipEvent_t ev_before, ev_after;
 };
 hipError_t launch_project(const ProjectArgs &a, hipStream_t s);
-// The finish kernel alone, over a.n_tok tokens of a.part (splits partials
-// [splits][n_tok][n_a + n_b] fp32): a prefill-sized step's GEMM output.
-hipError_t launch_project_finish(const ProjectArgs &a, hipStream_t s);
 hipError_t launch_out_project(const ProjectArgs &a, hipStream_t s);
+// Prefill-sized steps (more than kProjTokens tokens): one GEMM launch over
+// every token, tiles of kBigTileTokens tokens x one head's 256 weight rows,
+// with the finish kernel's epilogue (fp16 rounding, norm + RoPE, outputs,
+// cache rows) done by the workgroup that computed the tile (k_gemm.hip).
+// Needs (n_a + n_b) % 256 == 0 and hidden % 64 == 0; a.tok0 = 0.
+constexpr int kBigTileTokens = 256;
+constexpr int kBigProjMaxTokens = 1 << 24;
+hipError_t launch_project_big(const ProjectArgs &a, hipStream_t s);
 
 // Reference-compatible norm+RoPE on a contiguous [n_heads][head_dim] buffer.
 struct LegacyNormArgs {

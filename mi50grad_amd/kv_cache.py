@@ -174,12 +174,12 @@ class PagedKVCache:
                   table_rows, _ptr(q_out), _ptr(q_gate_out), _ptr(kv_out), stream)
 
     def project_path(self) -> str:
-        """Which path the last project_append took: "kernels" (libkvattn's
-        projection kernels, 64 tokens per launch pair) or "library_gemm"
-        (one hipBLASLt GEMM per weight matrix over up to 2048 tokens)."""
+        """Which path the last project_append took: "kernels" (the split-K
+        projection kernels, 64 tokens per launch pair) or "prefill_gemm" (one
+        GEMM launch over every token, the epilogue fused)."""
         p = ctypes.c_int32()
         _lib.call("kva_get_project_path", self.handle, ctypes.byref(p))
-        return {0: "kernels", 1: "library_gemm"}[p.value]
+        return {0: "kernels", 1: "prefill_gemm"}[p.value]
 
     def out_project(self, attn, n_tok: int, q_dim: int, w_o, n_out: int, out, residual=None,
                     stream=None) -> None:

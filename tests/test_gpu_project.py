@@ -11,11 +11,11 @@ append, against the oracle's producer (oracle.project_append).
   row the projected V; decode over the result within 2e-3 of fp32.
 * Chunking (steps of more than 64 tokens), the hidden sizes that select 1, 2
   and 4 splits, one-token steps, and the validation errors.
-* Prefill-sized steps (more than 64 tokens) go through one library GEMM per
-  weight matrix and the finish kernel: the same contract (bit-exact on
-  exact inputs, within one ulp plus the accumulation term on random ones)
-  at 70-300 tokens and at 1024 tokens of hidden 5120 (two config-4
-  sequences), and the path taken is reported.
+* Prefill-sized steps (more than 64 tokens) go through the prefill GEMM
+  (tiles of 128 tokens x one head, the norm/RoPE/append epilogue fused): the
+  same contract (bit-exact on exact inputs, within one ulp plus the
+  accumulation term on random ones) at 70-300 tokens and at 1024 tokens of
+  hidden 5120 (two config-4 sequences), and the path taken is reported.
 """
 import numpy as np
 import pytest
@@ -163,13 +163,13 @@ def test_project_chunks_and_splits(device, hidden, n_new):
     assert np.array_equal(got["g"].view(np.uint16), gate.view(np.uint16))
     assert np.array_equal(got["q"].view(np.uint16), q.view(np.uint16))
     _check_cache_rows(cache, kr, vr, lengths, n_new, k, v)
-    assert cache.project_path() == ("library_gemm" if sum(n_new) > 64 else "kernels")
+    assert cache.project_path() == ("prefill_gemm" if sum(n_new) > 64 else "kernels")
     cache.destroy()
 
 
 def test_project_prefill_sized_step(device):
     """Two config-4 sequences (P = 256 and 1024) each appending a 512-token
-    chunk, hidden 5120: 1024 tokens through the library GEMM; random inputs
+    chunk, hidden 5120: 1024 tokens through the prefill GEMM; random inputs
     within one fp16 ulp (+ the fp32 accumulation term) of the correctly
     rounded projection, Q within two ulps after norm + RoPE, cache rows
     bit-exact given the projected K/V; then an exact-input step of 300
@@ -179,7 +179,7 @@ def test_project_prefill_sized_step(device):
     say("project_append prefill-sized: 2 x 512 tokens, hidden 5120")
     tables = Tables(device, 2048)
     cache, kr, vr, exp, got, pos, qw, kw, _ = _run(device, rng, lengths, n_new, 5120, False, tables)
-    assert cache.project_path() == "library_gemm"
+    assert cache.project_path() == "prefill_gemm"
     q, gate, k_raw, k, v = exp
     for name, g, e in (("k", got["kv"][:, 0], k_raw), ("v", got["kv"][:, 1], v), ("gate", got["g"], gate)):
         diff = np.abs(g.astype(np.float32) - e.astype(np.float32))
@@ -199,7 +199,7 @@ def test_project_prefill_sized_step(device):
     say("project_append prefill-sized exact: 300 tokens, hidden 1024")
     cache, kr, vr, exp, got, pos, qw, kw, _ = _run(device, rng, [40, 0, 700], [100, 150, 50], 1024, True,
                                                     Tables(device, 1024))
-    assert cache.project_path() == "library_gemm"
+    assert cache.project_path() == "prefill_gemm"
     q, gate, k_raw, k, v = exp
     assert np.array_equal(got["kv"][:, 0].view(np.uint16), k_raw.view(np.uint16))
     assert np.array_equal(got["kv"][:, 1].view(np.uint16), v.view(np.uint16))
