@@ -7,39 +7,48 @@
 // then normalises, rotates and appends per token.  Here
 //   Y[t][n] = sum_k X[t][k] W[n][k]   (X: [T][hidden], W: the stacked
 //   weight rows [w_a; w_b], both k-contiguous)
-// runs as tiles of 128 tokens x 256 weight rows.  256 rows are exactly one
+// runs as tiles of 256 tokens x 256 weight rows.  256 rows are exactly one
 // head of one kind (Q, Q_gate, K or V), so the workgroup that finishes a
-// tile holds complete head rows for its 128 tokens and does the epilogue of
+// tile holds complete head rows for its 256 tokens and does the epilogue of
 // proj_finish_kernel itself: each value rounded to fp16 (what the
 // reference's GEMM stores), then Q -> RMSNorm + RoPE -> q_out, Q_gate ->
 // gate_out, K -> RMSNorm + RoPE -> its page slot (and K, V as projected ->
 // kv_out), V -> its page slot.  No [T][N] intermediate and no second launch.
 //
-// Main loop.  Eight waves in a 2 x 4 grid, each 64 tokens x 64 rows as
-// 4 x 4 tiles of v_mfma_f32_16x16x32_f16 (A = X rows, B = W rows; lane l
+// Main loop.  Eight waves in a 2 x 4 grid, each 128 tokens x 64 rows as
+// 8 x 4 tiles of v_mfma_f32_16x16x32_f16 (A = X rows, B = W rows; lane l
 // holds row l%16 and k-slots 8*(l/16)..+7 of both, C: tokens 4*(l/16)+i,
-// row l%16).  K goes in chunks of 64 through a ring of three LDS stages
-// (X 16 KB + W 32 KB each): buffer loads write LDS directly, chunk c+2 is
-// issued while chunk c is multiplied, one barrier per chunk makes a chunk
-// visible and frees the stage of chunk c-1.  Rows sit 128 bytes apart in
-// LDS with their 16-byte granules XOR-swizzled by (row & 7), chosen by which
-// global granule each lane fetches, so the 16 rows an MFMA operand read
-// touches fall in different banks.  A chunk issued past the end goes
-// through an empty buffer resource: the same loads, no memory access, so
-// every wave's load counter advances alike and the waits stay exact.
+// row l%16).  K goes in chunks of 64 through two LDS stages (X 32 KB + W
+// 32 KB each): buffer loads write LDS directly, chunk c+1 is issued while
+// chunk c is multiplied, one barrier per chunk makes a chunk visible and
+// frees the stage of chunk c-1.  A chunk of 64 k is one whole 128-byte line
+// per row, which the load path moves markedly faster than half lines (a
+// 32-wide chunk in four stages is slower although more of it is in
+// flight).  Rows sit 128 bytes apart in LDS with their 16-byte granules
+// XOR-swizzled (g_swizzle), chosen by which global granule each lane
+// fetches, so the 16 rows an MFMA operand read touches fall in different
+// banks.  A chunk issued past the end goes through an empty buffer
+// resource: the same loads, no memory access, so every wave's load counter
+// advances alike and the waits stay exact.
+//
+// What bounds it: the global -> LDS path.  A 256 x 256 tile needs 1/64 byte
+// per MAC, about 67 GB/s per CU to keep the MFMA pipes full at the clock
+// this kernel runs at; the load path alone moves ~45-51 GB/s per CU here.
 //
 // Tile order.  Tiles are numbered head-major (head, token tile) and dealt
 // out XCD by XCD (workgroup i runs on XCD i % 8): each XCD takes a
 // contiguous run of heads with all their token tiles, so a head's weight
-// rows are read from HBM by one XCD and reused from its L2 by the token
-// tiles running beside each other.
+// rows are read by one XCD and reused from its L2 by the token tiles
+// running beside each other.
 #include "k_common.h"
 #include "k_normrope.h"
 #include "kva_internal.h"
 
+// Chunk width in k, LDS stages, waves per workgroup (tuning builds may
+// override all three together).
 #ifndef KVA_GEMM_KC
-#define KVA_GEMM_KC 32
-#define KVA_GEMM_S 4
+#define KVA_GEMM_KC 64
+#define KVA_GEMM_S 2
 #define KVA_GEMM_W 8
 #endif
 
@@ -70,14 +79,19 @@ struct GRing {
     static constexpr int kLoads = kLoadsX + kLoadsW;
 };
 
-// The granule swizzle of row r: the rows an MFMA operand read touches at
-// one logical granule land on distinct bank groups whether the LDS serves
-// 8 lanes per 128-byte cycle or 16 per 256-byte cycle (the counters read
-// zero bank conflicts with it, 27.5 M cycles per launch with the granule
-// XORed by the row's 256-byte cycle alone).
+// The granule swizzle of row r.  The 16 rows one MFMA operand read touches
+// at one logical granule must land on distinct 16-byte bank groups whether
+// the LDS serves 8 lanes per 128-byte cycle or 16 per 256-byte cycle.  With
+// 128-byte rows (KC = 64) two rows share a 256-byte cycle, so the even rows
+// take granules 0..7 and the odd rows the same set XORed by 4; with 64-byte
+// rows (KC = 32) four rows share one.  The counters read zero bank
+// conflicts for both.
 template <int KC>
 __device__ __forceinline__ int g_swizzle(int r) {
-    return ((r >> 1) ^ (r >> 2)) & (KC / 8 - 1);
+    if constexpr (KC == 64)
+        return ((r >> 1) ^ ((r & 1) << 2)) & 7;
+    else
+        return ((r >> 1) ^ (r >> 2)) & (KC / 8 - 1);
 }
 
 // LDS byte offset of row r's 16-byte granule g within a stage's X or W part.
@@ -170,6 +184,8 @@ __global__ __launch_bounds__(64 * W) void proj_big_kernel(ProjectArgs a) {
 #pragma unroll
     for (int s = 0; s + 1 < S; ++s) issue(s);
     for (int c = 0; c < nc; ++c) {
+        // Chunk c has landed once no more than S - 2 later chunks' loads
+        // are outstanding; the barrier then also frees chunk c-1's stage.
         wait_vm<R::kLoads * (S - 2)>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
@@ -204,18 +220,38 @@ __global__ __launch_bounds__(64 * W) void proj_big_kernel(ProjectArgs a) {
     __syncthreads();
 
     const int H = a.num_heads, hkv = a.num_kv_heads;
-    const int hw = threadIdx.x >> 5;  // half-wave 0..15
+    const int hw = threadIdx.x >> 5;  // half-wave 0 .. 2W-1
     const int l32 = threadIdx.x & 31;
     const bool is_q = head < H, is_gate = !is_q && head < 2 * H;
     const int kv = head - 2 * H;  // K heads 0..hkv-1, then V heads
     const bool rot = is_q || (!is_gate && kv < hkv);
     uint16_t *epi = reinterpret_cast<uint16_t *>(ring);
+    // The norm weights are the same for every row of the tile; each
+    // half-wave's cos/sin rows are requested before the half is written, so
+    // the finish loop waits on none of them row by row.
+    constexpr int kRowsPerHw = kGWaveTok / (2 * W);
+    NormRopeIn nin[kRowsPerHw];
+    const uint4 wnorm = rot ? ld16((is_q ? a.q_w : a.k_w) + 8 * l32) : make_uint4(0, 0, 0, 0);
+    const int cl = a.half_rot > 0 ? min(l32, a.half_rot / 4 - 1) : 0;
     // Two halves: the waves of token half `half` write their sums as fp16
     // (each rounded once: what the reference's GEMM stores) into the tile
     // [kGWaveTok tokens][256 rows]; tile (m, n), C row 4*grp + e is token
-    // 16*m + 4*grp + e of the half, column col is row 64*wn + 16*n + col.
-    // Then every wave finishes the half's token rows.
+    // 16*m + 4*grp + e of the half, column col is row kWaveRows*wn + 16*n +
+    // col.  Then every wave finishes the half's token rows.
     for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int j = 0; j < kRowsPerHw; ++j) {
+            nin[j].w = wnorm;
+            nin[j].c = make_uint2(0, 0);
+            nin[j].s = make_uint2(0, 0);
+            if (rot && a.half_rot > 0) {
+                // Tokens past the launch's end carry the last token's
+                // position, so these reads stay inside the tables.
+                const size_t off = static_cast<size_t>(meta[0][half * kGWaveTok + hw + 2 * W * j]) * a.half_rot;
+                nin[j].c = ld8(a.cos_tab + off + 4 * cl);
+                nin[j].s = ld8(a.sin_tab + off + 4 * cl);
+            }
+        }
         if (wm == half) {
 #pragma unroll
             for (int m = 0; m < kGTM; ++m)
@@ -230,7 +266,9 @@ __global__ __launch_bounds__(64 * W) void proj_big_kernel(ProjectArgs a) {
         __syncthreads();
         // Finish: one 32-lane group per token row, 8 dims per lane, the
         // arithmetic of proj_finish_kernel (norm_rope_apply: the same bits).
-        for (int rr = hw; rr < kGWaveTok; rr += 2 * W) {
+#pragma unroll
+        for (int j = 0; j < kRowsPerHw; ++j) {
+            const int rr = hw + 2 * W * j;
             const int r = half * kGWaveTok + rr;
             const int tl = t0 + r;
             if (tl >= a.n_tok) break;
@@ -241,14 +279,7 @@ __global__ __launch_bounds__(64 * W) void proj_big_kernel(ProjectArgs a) {
                 continue;
             }
             if (!is_q && a.kv_out) st16(a.kv_out + (static_cast<size_t>(t) * 2 * hkv + kv) * kHeadDim + 8 * l32, y);
-            uint4 o = y;
-            if (rot) {
-                const int pos = meta[0][r];
-                const NormRopeIn nin =
-                    norm_rope_in<32>(is_q ? a.q_w : a.k_w, a.cos_tab + static_cast<size_t>(pos) * a.half_rot,
-                                     a.sin_tab + static_cast<size_t>(pos) * a.half_rot, a.half_rot, l32);
-                o = norm_rope_apply<32>(y, nin, a.half_rot, a.eps, l32);
-            }
+            const uint4 o = rot ? norm_rope_apply<32>(y, nin[j], a.half_rot, a.eps, l32) : y;
             if (is_q) {
                 st16(a.q_out + (static_cast<size_t>(t) * H + head) * kHeadDim + 8 * l32, o);
                 continue;
