@@ -227,3 +227,73 @@ def test_graph_replay_project_append(device):
     stream.destroy()
     eager.destroy()
     graphed.destroy()
+
+
+def test_graph_replay_prefill_sized_project(device):
+    """A prefill-sized step (130 new tokens: kva_project_append takes the
+    prefill GEMM, one launch with its norm/RoPE/append epilogue) recorded
+    once and replayed for five more steps with fresh x: every replay's q,
+    gate and K/V outputs equal the eager twin's and the oracle's bit for bit
+    (fp32-exact inputs), and at the end so do the pools."""
+    say("graph replay of a prefill-sized project_append")
+    rng = np.random.default_rng(9)
+    lengths, n_new, hidden, steps = [30, 47, 3], [50, 40, 40], 512, 6
+    B, T = len(lengths), sum(n_new)
+    ids, o = [], 0
+    for L, n in zip(lengths, n_new):
+        k = (L + steps * n + 15) // 16
+        ids.append(list(range(o, o + k))[::-1])
+        o += k
+    eager, graphed = [build_cache(lengths, ids, extra_rows=[steps * n for n in n_new],
+                                  rng=np.random.default_rng(13))[0] for _ in range(2)]
+    tables = Tables(device, 512)
+    stream = Stream()
+    wq = (rng.integers(-2, 3, (2 * H * D, hidden), dtype=np.int8) * 2.0 ** -7).astype(np.float16)
+    wkv = (rng.integers(-2, 3, (2 * HKV * D, hidden), dtype=np.int8) * 2.0 ** -7).astype(np.float16)
+    qw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    kw = (1 + 0.02 * rng.standard_normal(D, dtype=np.float32)).astype(np.float16)
+    w = [device.array(a) for a in (wq, wkv, qw, kw)]
+    bufs = [dict(x=device.empty((T, hidden), np.float16), q=device.empty((T, H, D), np.float16),
+                 g=device.empty((T, H, D), np.float16), kv=device.empty((T, 2, HKV, D), np.float16))
+            for _ in range(2)]
+
+    def call(cache, b, stream_h):
+        cache.project_append(0, b["x"], hidden, *w, tables.d_cos, tables.d_sin, tables.rows, b["q"], b["g"],
+                             b["kv"], stream=stream_h)
+
+    graph = None
+    for step in range(steps):
+        x = rng.integers(-3, 4, (T, hidden), dtype=np.int8).astype(np.float16)
+        for b in bufs:
+            device.upload(b["x"].ptr, x.tobytes())
+        device.synchronize()
+        eager.begin_step(list(range(B)), n_new)
+        call(eager, bufs[0], None)
+        graphed.begin_step(list(range(B)), n_new, stream=stream.handle)
+        if graph is None:
+            graph = graphed.record_step(stream.handle)
+            call(graphed, bufs[1], stream.handle)
+            graph.end()
+        graph.launch()
+        stream.synchronize()
+        device.synchronize()
+        assert eager.project_path() == "prefill_gemm"
+        pos = [L + step * n + i for L, n in zip(lengths, n_new) for i in range(n)]
+        q, gate, k_raw, _, v = orc.project_append(x, wq, wkv, qw, kw, tables.cos[pos], tables.sin[pos])
+        for name, exp in (("q", q), ("g", gate)):
+            got = bufs[1][name].numpy().view(np.uint16)
+            assert np.array_equal(got, bufs[0][name].numpy().view(np.uint16)), (step, name)
+            assert np.array_equal(got, exp.view(np.uint16)), (step, name)
+        kv = bufs[1]["kv"].numpy()
+        assert np.array_equal(kv.view(np.uint16), bufs[0]["kv"].numpy().view(np.uint16)), step
+        assert np.array_equal(kv[:, 0].view(np.uint16), k_raw.view(np.uint16)), step
+        assert np.array_equal(kv[:, 1].view(np.uint16), v.view(np.uint16)), step
+    ke, ve = eager.download_pools(0)
+    kg, vg = graphed.download_pools(0)
+    assert np.array_equal(ke.view(np.uint16), kg.view(np.uint16))
+    assert np.array_equal(ve.view(np.uint16), vg.view(np.uint16))
+    graph.destroy()
+    stream.synchronize()
+    stream.destroy()
+    eager.destroy()
+    graphed.destroy()

@@ -12,7 +12,7 @@ append, against the oracle's producer (oracle.project_append).
 * Chunking (steps of more than 64 tokens), the hidden sizes that select 1, 2
   and 4 splits, one-token steps, and the validation errors.
 * Prefill-sized steps (more than 64 tokens) go through the prefill GEMM
-  (tiles of 128 tokens x one head, the norm/RoPE/append epilogue fused): the
+  (tiles of 256 tokens x one head, the norm/RoPE/append epilogue fused): the
   same contract (bit-exact on exact inputs, within one ulp plus the
   accumulation term on random ones) at 70-300 tokens and at 1024 tokens of
   hidden 5120 (two config-4 sequences), and the path taken is reported.
@@ -231,13 +231,16 @@ def test_project_optional_outputs(device):
     cache.destroy()
 
 
-def test_project_other_head_shape(device):
+@pytest.mark.parametrize("n_new", [[2, 1, 5], [120, 1, 200]])
+def test_project_other_head_shape(device, n_new):
     """8 query and 2 kv heads (G = 4): 5120 weight rows, so the last group
     of 7 row tiles is partial (its missing tiles are loaded, never
-    written); every output still bit-exact on fp32-exact inputs."""
+    written); every output still bit-exact on fp32-exact inputs.  321 new
+    tokens take the prefill GEMM instead: 20 heads of four kinds, the second
+    token tile 65 tokens long."""
     rng = np.random.default_rng(35)
     h, hkv, hidden = 8, 2, 1024
-    lengths, n_new = [19, 250, 64], [2, 1, 5]
+    lengths = [19, 250, 64]
     T = sum(n_new)
     ids = _ids(rng, [(L + n + 15) // 16 for L, n in zip(lengths, n_new)])
     say("project_append with 8 q / 2 kv heads")
@@ -262,4 +265,5 @@ def test_project_other_head_shape(device):
     assert np.array_equal(kvo[:, 0].view(np.uint16), k_raw.view(np.uint16))
     assert np.array_equal(kvo[:, 1].view(np.uint16), v.view(np.uint16))
     _check_cache_rows(cache, kr, vr, lengths, n_new, k, v)
+    assert cache.project_path() == ("prefill_gemm" if T > 64 else "kernels")
     cache.destroy()
