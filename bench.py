@@ -603,17 +603,27 @@ def c4_workload(dev, steps, warmup):
     inputs = make_inputs(dev, T)
     seqs = list(range(B))
 
-    def step(evs=None, kernel=False):
+    def step(evs=None, kernel=False, mode="fused"):
+        # fused: kva_append_prefill (append + attention, one call) in the
+        # bracket; two: kva_append_qknorm_rope + kva_prefill in the bracket;
+        # prefill: kva_prefill alone, the append before the bracket (how
+        # earlier lines were measured).
         for b in seqs:
             cache.set_len(b, prefix[b])
         cache.begin_step(seqs, chunk)
         for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
-            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
+            if mode == "prefill":
+                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
             if evs is not None and kernel:
                 cache.kernel_events(evs[layer][0], evs[layer][1])  # mq_kernel alone
             elif evs is not None:
                 evs[layer][0].record()
-            cache.prefill(layer, q, out)
+            if mode == "fused":
+                cache.append_prefill(layer, q, k, v, qw, kw, d_cos, d_sin, 4096, out)
+            else:
+                if mode == "two":
+                    cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
+                cache.prefill(layer, q, out)
             if evs is not None and not kernel:
                 evs[layer][1].record()
         if kernel:
@@ -624,19 +634,21 @@ def c4_workload(dev, steps, warmup):
     dev.synchronize()
     evs = [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
     flush = L2Flush(dev)
-    wall = 0.0
-    for i in range(steps):
-        flush()  # each step starts from HBM: its 1.3 GB would not fit the MALL anyway
-        t0 = time.perf_counter()
-        step(evs[i])
-        dev.synchronize()
-        wall += time.perf_counter() - t0
-    ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s]
-    for i in range(steps):  # mq_kernel's own duration, in steps of their own
-        flush()
-        step(evs[i], kernel=True)
-        dev.synchronize()
-    kms = [e[0].elapsed_ms(e[1]) for s in evs for e in s]
+
+    def timed(mode, kernel=False):
+        wall = 0.0
+        for i in range(steps):
+            flush()  # each step starts from HBM: its 1.3 GB would not fit the MALL anyway
+            t0 = time.perf_counter()
+            step(evs[i], kernel, mode)
+            dev.synchronize()
+            wall += time.perf_counter() - t0
+        return [e[0].elapsed_ms(e[1]) for s in evs for e in s], wall
+
+    ms, wall = timed("fused")
+    kms, _ = timed("fused", kernel=True)  # mq_kernel's own duration, in steps of their own
+    two_ms, _ = timed("two")
+    pre_ms, _ = timed("prefill")
     for s in evs:
         for pair in s:
             for x in pair:
@@ -644,9 +656,12 @@ def c4_workload(dev, steps, warmup):
     flush.free()
     cache.destroy()
     flops = 4 * H * D * sum(sum(p + i + 1 for i in range(c)) for p, c in zip(prefix, chunk))
-    by = (sum(p + c for p, c in zip(prefix, chunk)) * ROW_BYTES + 2 * T * H * D * 2)
+    # Cache rows read, q read and out written, the new K/V rows read and
+    # written to their slots.
+    by = (sum(p + c for p, c in zip(prefix, chunk)) * ROW_BYTES + 2 * T * H * D * 2 + 4 * T * HKV * D * 2)
     return {"wall_s": wall, "steps": steps, "tokens": T, "flops_per_layer": flops, "bytes_per_layer": by,
-            "prefill_avg_us": float(np.mean(ms) * 1e3), "kernel_avg_us": float(np.mean(kms) * 1e3)}
+            "prefill_avg_us": float(np.mean(ms) * 1e3), "kernel_avg_us": float(np.mean(kms) * 1e3),
+            "two_calls_avg_us": float(np.mean(two_ms) * 1e3), "prefill_only_avg_us": float(np.mean(pre_ms) * 1e3)}
 
 
 def c5_workload(dev, steps, warmup, layers=4, batch=64):
@@ -1006,14 +1021,17 @@ def workload_line(dev, args) -> dict:
         ms = r["wall_s"] * 1e3 / r["steps"]
         extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c4()}
         return ({**extra, 
-            "metric": "config-4 chunked prefill attention TFLOP/s (pp512 after 0/256/1024/2048 rows, B=4)",
+            "metric": "config-4 chunked prefill TFLOP/s, K/V append + causal attention (pp512 after 0/256/1024/2048 rows, B=4)",
             "value": tflops, "unit": "TFLOP/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "dtype": "f16", "data": "synthetic",
             "config": {"workload": "C4", "layers": LAYERS, "tokens_per_step": r["tokens"]},
             "tok_per_s": r["tokens"] * r["steps"] / r["wall_s"],
             "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("prefill_c4_traffic.json"),
-                         "kernel": "kva_prefill = mq_kernel<1 tile, 8 waves, causal, 64-key blocks> + mq_combine_kernel",
+                         "kernel": "kva_append_prefill = append_kernel + mq_kernel<1 tile, 8 waves, causal, "
+                                   "64-key blocks> + mq_combine_kernel",
+                         "two_calls_avg_us": r["two_calls_avg_us"],
+                         "prefill_only_avg_us": r["prefill_only_avg_us"],
                          "mq_kernel": {"what": "mq_kernel alone: HIP events the library records around its launch "
                                                "(kva_kernel_events), in a second set of as many steps",
                                        "avg_us": r["kernel_avg_us"], "achieved": kernel_tflops,
@@ -1108,6 +1126,8 @@ def other_configs(dev, args) -> dict:
                          "two_calls_us_per_step": d["two_calls_per_layer"]["step_us"],
                          "launches_per_step": d["launches_per_step"], "timing": d["timing"]},
         "c4": lambda d: {"tflops": d["value"], "frac": d["roofline"]["frac"], "avg_us": d["roofline"]["avg_us"],
+                         "two_calls_avg_us": d["roofline"]["two_calls_avg_us"],
+                         "prefill_only_avg_us": d["roofline"]["prefill_only_avg_us"],
                          "mq_kernel_frac": d["roofline"]["mq_kernel"]["frac"],
                          "mq_kernel_avg_us": d["roofline"]["mq_kernel"]["avg_us"],
                          "tok_per_s": d["tok_per_s"], "mfma_busy": d["roofline"]["mfma_busy"]},

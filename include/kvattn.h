@@ -272,6 +272,26 @@ int kva_prefill_gated(kva_cache *cache, int32_t layer, const void *q, const void
                       int64_t gate_stride, void *out, kva_stream_t stream);
 int kva_tree_verify_gated(kva_cache *cache, int32_t layer, const void *q, const void *gate,
                           int64_t gate_stride, void *out, kva_stream_t stream);
+/* kva_append_qknorm_rope followed by kva_prefill in one call: the
+ * per-token qknorm_rope launches for Q and K, the K/V copy into the cache
+ * and the causal flash attention of _prefill_full_attention
+ * (engine.py:3087-3117; qknorm_rope.hip:55-162, flash_attn_256.hip:38-137).
+ * Two launches on `stream`: the append (q normalised and rotated in place,
+ * as kva_append_decode does; K normalised into its cache slots, k itself
+ * only read; V copied) and the attention.  out and the cache rows are
+ * bit-identical to kva_append_qknorm_rope + kva_prefill.  Arguments as
+ * kva_append_qknorm_rope, out as kva_prefill.  Not while a graph is
+ * recorded (as kva_prefill).                                               */
+int kva_append_prefill(kva_cache *cache, int32_t layer, void *q, const void *k, const void *v,
+                       const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                       const void *sin_tab, int32_t table_rows, void *out, kva_stream_t stream);
+/* kva_append_prefill with the output gate of kva_prefill_gated (the
+ * sigmoid_mul at engine.py:3120-3121).                                     */
+int kva_append_prefill_gated(kva_cache *cache, int32_t layer, void *q, const void *k,
+                             const void *v, const void *q_norm_w, const void *k_norm_w,
+                             const void *cos_tab, const void *sin_tab, int32_t table_rows,
+                             const void *gate, int64_t gate_stride, void *out,
+                             kva_stream_t stream);
 /* Keep accepted tree rows and drop the rest, in every layer: for sequence
  * seq_ids[b], rows base_len[b] + keep_rows[j] (j in [keep_off[b],
  * keep_off[b+1]), strictly increasing) move to base_len[b] + (j -

@@ -76,6 +76,8 @@ SIGNATURES = {
     "kva_prefill": [_P, _I, _P, _P, _P],
     "kva_tree_verify": [_P, _I, _P, _P, _P],
     "kva_prefill_gated": [_P, _I, _P, _P, c_int64, _P, _P],
+    "kva_append_prefill": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P],
+    "kva_append_prefill_gated": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, c_int64, _P, _P],
     "kva_tree_verify_gated": [_P, _I, _P, _P, c_int64, _P, _P],
     "kva_rollback": [_P, _I, _PI, _PI, _PI, _PI, _P],
     "kva_set_decode_split": [_P, _I],

@@ -1231,9 +1231,12 @@ int kva_decode_gated(kva_cache *c, int32_t layer, const void *q, const void *gat
     return capture_note(c, decode_impl(c, layer, q, gate, gate_stride, out, stream));
 }
 
+// Causal prefill or tree verify over the step; with `append`
+// (kva_append_prefill) the step's append launch goes first.
 static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kva_stream_t stream,
-                       bool tree, const void *gate = nullptr, int64_t gate_stride = 0) {
-    if (int rc = refuse_while_capturing(c, tree ? "kva_tree_verify" : "kva_prefill")) return rc;
+                       bool tree, const void *gate = nullptr, int64_t gate_stride = 0,
+                       const kva::AppendArgs *append = nullptr, const char *what = nullptr) {
+    if (int rc = refuse_while_capturing(c, what ? what : tree ? "kva_tree_verify" : "kva_prefill")) return rc;
     if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
     int rc = check_layer(c, layer);
     if (rc) return rc;
@@ -1244,6 +1247,7 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     if ((rc = check_gate(gate, gate_stride, c->cfg.num_heads))) return rc;
     if ((rc = require_device(c))) return rc;
     if (c->st_n_tok == 0) return KVA_OK;
+    if (append) KVA_HIP(kva::launch_append(*append, static_cast<hipStream_t>(stream)));
     kva::MultiQueryArgs a{};
     a.gate = static_cast<const uint16_t *>(gate);
     a.gate_stride = gate_stride;
@@ -1303,6 +1307,39 @@ int kva_tree_verify_gated(kva_cache *c, int32_t layer, const void *q, const void
                           void *out, kva_stream_t stream) {
     if (!gate) return fail(KVA_ERR_INVALID_ARG, "NULL gate");
     return multi_query(c, layer, q, out, stream, true, gate, gate_stride);
+}
+
+static int append_prefill_impl(kva_cache *c, int32_t layer, void *q, const void *k, const void *v,
+                               const void *q_norm_w, const void *k_norm_w, const void *cos_tab,
+                               const void *sin_tab, int32_t table_rows, const void *gate, int64_t gate_stride,
+                               void *out, kva_stream_t stream, const char *what) {
+    if (int rc = refuse_while_capturing(c, what)) return rc;
+    if (!c) return fail(KVA_ERR_INVALID_ARG, "cache is NULL");
+    int rc = check_layer(c, layer);
+    if (rc) return rc;
+    if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
+    kva::AppendArgs ap;
+    if ((rc = make_append(c, layer, q, const_cast<void *>(k), v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows,
+                          ap)))
+        return rc;
+    ap.keep_k = 1;  // k is only read; the cache gets the normalised rows
+    return multi_query(c, layer, q, out, stream, false, gate, gate_stride, &ap, what);
+}
+
+int kva_append_prefill(kva_cache *c, int32_t layer, void *q, const void *k, const void *v,
+                       const void *q_norm_w, const void *k_norm_w, const void *cos_tab, const void *sin_tab,
+                       int32_t table_rows, void *out, kva_stream_t stream) {
+    return append_prefill_impl(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, nullptr, 0,
+                               out, stream, "kva_append_prefill");
+}
+
+int kva_append_prefill_gated(kva_cache *c, int32_t layer, void *q, const void *k, const void *v,
+                             const void *q_norm_w, const void *k_norm_w, const void *cos_tab, const void *sin_tab,
+                             int32_t table_rows, const void *gate, int64_t gate_stride, void *out,
+                             kva_stream_t stream) {
+    if (!gate) return fail(KVA_ERR_INVALID_ARG, "NULL gate");
+    return append_prefill_impl(c, layer, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows, gate,
+                               gate_stride, out, stream, "kva_append_prefill_gated");
 }
 
 int kva_rollback(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const int32_t *base_len,

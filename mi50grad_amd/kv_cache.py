@@ -162,6 +162,20 @@ class PagedKVCache:
                       _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab), table_rows, _ptr(gate), stride, _ptr(out),
                       stream)
 
+    def append_prefill(self, layer: int, q, k, v, q_norm_w, k_norm_w, cos_tab, sin_tab, table_rows: int, out,
+                       stream=None, gate=None, gate_stride: int = 0) -> None:
+        """append() then prefill() in one call (kva_append_prefill): q is
+        normalised in place, k only read; out and the cache rows are
+        bit-identical to the two calls."""
+        if gate is None:
+            _lib.call("kva_append_prefill", self.handle, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_w),
+                      _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab), table_rows, _ptr(out), stream)
+        else:
+            stride = gate_stride or self.num_heads * 256
+            _lib.call("kva_append_prefill_gated", self.handle, layer, _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_w),
+                      _ptr(k_norm_w), _ptr(cos_tab), _ptr(sin_tab), table_rows, _ptr(gate), stride, _ptr(out),
+                      stream)
+
     def project_append(self, layer: int, x, hidden: int, w_q_fused, w_kv_fused, q_norm_w, k_norm_w,
                        cos_tab, sin_tab, table_rows: int, q_out, q_gate_out=None, kv_out=None,
                        stream=None) -> None:

@@ -336,6 +336,41 @@ def test_multi_query_refusals_before_device():
     c.destroy()
 
 
+def test_append_prefill_refusals_before_device():
+    """kva_append_prefill validates the append's and the attention's
+    arguments (pointers, alignment, table rows, gate) before the device
+    check, which a valid call on a host-only cache reaches last."""
+    c = make(num_heads=24, num_kv_heads=4)
+    _rows(c, [0, 1], [10, 20])
+    args = [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64]
+    with pytest.raises(KvaError, match="no step") as e:
+        c.append_prefill(0, *args, FAKE)
+    assert code(e) == -8
+    c.begin_step([0, 1], [3, 5])
+    for i, val, want in ((0, None, -1), (1, FAKE + 8, -10), (3, FAKE + 2, -10), (5, FAKE + 4, -10), (7, 20, -1)):
+        bad = list(args)
+        bad[i] = val
+        with pytest.raises(KvaError) as e:
+            c.append_prefill(0, *bad, FAKE)
+        assert code(e) == want, (i, val)
+    with pytest.raises(KvaError) as e:
+        c.append_prefill(0, *args, FAKE + 2)  # misaligned out
+    assert code(e) == -10
+    with pytest.raises(KvaError, match="NULL gate"):
+        _lib.call("kva_append_prefill_gated", c.handle, 0, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 64, None, 0,
+                  FAKE, None)
+    with pytest.raises(KvaError) as e:
+        c.append_prefill(0, *args, FAKE, gate=FAKE, gate_stride=24 * 256 - 4)
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        c.append_prefill(5, *args, FAKE)  # layer out of range
+    assert code(e) == -1
+    with pytest.raises(KvaError) as e:
+        c.append_prefill(0, *args, FAKE)
+    assert code(e) == -3
+    c.destroy()
+
+
 def test_legacy_decode_without_workspace_refuses_long_caches():
     """kva_legacy_decode with no workspace cache runs only the whole-sequence
     form; past 1024 rows it refuses (KVA_ERR_STATE) instead of streaming a
