@@ -632,27 +632,28 @@ def c4_workload(dev, steps, warmup):
     for _ in range(warmup):
         step()
     dev.synchronize()
-    evs = [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
     flush = L2Flush(dev)
 
-    def timed(mode, kernel=False):
-        wall = 0.0
-        for i in range(steps):
+    # The modes take turns step by step, so each sees the same clock and
+    # thermal state; mq_kernel's own duration comes from steps of their own.
+    modes = (("fused", False), ("fused", True), ("two", False), ("prefill", False))
+    evs = {m: [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)] for m in modes}
+    wall = 0.0
+    for i in range(steps):
+        for m in modes:
             flush()  # each step starts from HBM: its 1.3 GB would not fit the MALL anyway
             t0 = time.perf_counter()
-            step(evs[i], kernel, mode)
+            step(evs[m][i], m[1], m[0])
             dev.synchronize()
-            wall += time.perf_counter() - t0
-        return [e[0].elapsed_ms(e[1]) for s in evs for e in s], wall
-
-    ms, wall = timed("fused")
-    kms, _ = timed("fused", kernel=True)  # mq_kernel's own duration, in steps of their own
-    two_ms, _ = timed("two")
-    pre_ms, _ = timed("prefill")
-    for s in evs:
-        for pair in s:
-            for x in pair:
-                x.destroy()
+            if m == modes[0]:
+                wall += time.perf_counter() - t0
+    per = {m: [e[0].elapsed_ms(e[1]) for s in evs[m] for e in s] for m in modes}
+    ms, kms, two_ms, pre_ms = (per[m] for m in modes)
+    for m in modes:
+        for s in evs[m]:
+            for pair in s:
+                for x in pair:
+                    x.destroy()
     flush.free()
     cache.destroy()
     flops = 4 * H * D * sum(sum(p + i + 1 for i in range(c)) for p, c in zip(prefix, chunk))
