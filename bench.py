@@ -582,7 +582,7 @@ def stored_mfma_busy() -> dict | None:
             "SQ_VALU_MFMA_BUSY_CYCLES per SIMD over the kernel's cycles (a stored profile)"}
 
 
-def c4_workload(dev, steps, warmup):
+def c4_workload(dev, steps, warmup, extras=True):
     """Config 4: 4 sequences append a 512-token chunk after 0/256/1024/2048
     cached rows (fused norm+RoPE+append), then causal prefill attention; 16
     layers per step.  Lengths are set back after each step."""
@@ -636,7 +636,8 @@ def c4_workload(dev, steps, warmup):
 
     # The modes take turns step by step, so each sees the same clock and
     # thermal state; mq_kernel's own duration comes from steps of their own.
-    modes = (("fused", False), ("fused", True), ("two", False), ("prefill", False))
+    modes = (("fused", False), ("fused", True), ("two", False), ("prefill", False)) if extras else \
+        (("fused", False),)
     evs = {m: [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)] for m in modes}
     wall = 0.0
     for i in range(steps):
@@ -648,7 +649,8 @@ def c4_workload(dev, steps, warmup):
             if m == modes[0]:
                 wall += time.perf_counter() - t0
     per = {m: [e[0].elapsed_ms(e[1]) for s in evs[m] for e in s] for m in modes}
-    ms, kms, two_ms, pre_ms = (per[m] for m in modes)
+    ms = per[modes[0]]
+    kms, two_ms, pre_ms = (per[m] for m in modes[1:]) if extras else (None, None, None)
     for m in modes:
         for s in evs[m]:
             for pair in s:
@@ -661,8 +663,9 @@ def c4_workload(dev, steps, warmup):
     # written to their slots.
     by = (sum(p + c for p, c in zip(prefix, chunk)) * ROW_BYTES + 2 * T * H * D * 2 + 4 * T * HKV * D * 2)
     return {"wall_s": wall, "steps": steps, "tokens": T, "flops_per_layer": flops, "bytes_per_layer": by,
-            "prefill_avg_us": float(np.mean(ms) * 1e3), "kernel_avg_us": float(np.mean(kms) * 1e3),
-            "two_calls_avg_us": float(np.mean(two_ms) * 1e3), "prefill_only_avg_us": float(np.mean(pre_ms) * 1e3)}
+            "prefill_avg_us": float(np.mean(ms) * 1e3),
+            **{k: (float(np.mean(v) * 1e3) if v is not None else None)
+               for k, v in (("kernel_avg_us", kms), ("two_calls_avg_us", two_ms), ("prefill_only_avg_us", pre_ms))}}
 
 
 def c5_workload(dev, steps, warmup, layers=4, batch=64):
@@ -1016,9 +1019,9 @@ def workload_line(dev, args) -> dict:
                          "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("project_c4_traffic.json"),
                          "avg_us": us, "alg_flops_per_launch": r["flops"]}})
     if args.workload == "c4":
-        r = c4_workload(dev, args.steps, args.warmup)
+        r = c4_workload(dev, args.steps, args.warmup, extras=not args.no_extras)
         tflops = r["flops_per_layer"] / (r["prefill_avg_us"] * 1e-6) / 1e12
-        kernel_tflops = r["flops_per_layer"] / (r["kernel_avg_us"] * 1e-6) / 1e12
+        kernel_tflops = (r["flops_per_layer"] / (r["kernel_avg_us"] * 1e-6) / 1e12) if r["kernel_avg_us"] else None
         ms = r["wall_s"] * 1e3 / r["steps"]
         extra = {} if args.no_cpu_baseline else {"cpu_baseline": cpu_baseline_c4()}
         return ({**extra, 
@@ -1036,7 +1039,7 @@ def workload_line(dev, args) -> dict:
                          "mq_kernel": {"what": "mq_kernel alone: HIP events the library records around its launch "
                                                "(kva_kernel_events), in a second set of as many steps",
                                        "avg_us": r["kernel_avg_us"], "achieved": kernel_tflops,
-                                       "frac": kernel_tflops / MFMA_PEAK_TFLOPS},
+                                       "frac": kernel_tflops / MFMA_PEAK_TFLOPS if kernel_tflops else None},
                          "avg_us": r["prefill_avg_us"], "alg_flops_per_launch": r["flops_per_layer"],
                          "alg_bytes_per_launch": r["bytes_per_layer"], "mfma_busy": stored_mfma_busy(),
                          "peak_derived": mfma_peak_derived()}})
@@ -1072,7 +1075,8 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=0, help="decode split tokens (0 = automatic)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
-                    help="c3: leave out the ctx8192 variant, the bandwidth probes and the other configs")
+                    help="c3: leave out the ctx8192 variant, the bandwidth probes and the other configs; "
+                         "c4: time the headline call only (no two-call, prefill-only or kernel-event steps)")
     ap.add_argument("--timeline", action="store_true",
                     help="c3/ctx8192: after the timed steps, record the decode kernels' per-workgroup "
                          "timeline (kva_timeline_enable) for one more step and add its summary")
