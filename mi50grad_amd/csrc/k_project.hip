@@ -237,6 +237,12 @@ __global__ __launch_bounds__(64 * WAVES) void proj_lds_kernel(ProjectArgs a) {
         load_to_lds(rs, dst + 1024, loff[1]);
     };
 
+    // The first DEPTH weight stages go out before x: the weights come from
+    // HBM and x from L2, so both are in flight together.  Taking delivery
+    // of x below then also waits for these stages (loads complete in
+    // order); the ring's waits are upper bounds and stay exact after that.
+#pragma unroll
+    for (int n = 0; n < DEPTH; ++n) issue(n);
     const auto xr = ro_rsrc(a.x, static_cast<uint32_t>(a.n_tok) * static_cast<uint32_t>(a.hidden) * 2u);
     uint4 xv[STEPS][NTB];
 #pragma unroll
@@ -260,8 +266,6 @@ __global__ __launch_bounds__(64 * WAVES) void proj_lds_kernel(ProjectArgs a) {
 #pragma unroll
         for (int j = 0; j < NTB; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-    for (int n = 0; n < DEPTH; ++n) issue(n);
     // A reads: row r at logical granule 4*s + g of a stage's two steps.
     const int sw = (r >> 1) & 7;
 #pragma unroll
