@@ -101,8 +101,8 @@ __device__ __forceinline__ uint32_t g_swz(int r, int g) {
 }
 
 // Issue one chunk's loads of this wave into `stage`: load j of the wave
-// covers LDS granule slots 64*(kGWaves*j + wv) + lane of the X part, then of
-// the W part; slot p holds row p / kGran at stored granule p % kGran, i.e.
+// covers LDS granule slots 64*(W*j + wv) + lane of the X part, then of the
+// W part; slot p holds row p / kGran at stored granule p % kGran, i.e.
 // global granule (p % kGran) ^ swizzle(row) of that row.
 template <int KC, int W>
 __device__ __forceinline__ void g_issue(uint32_t stage, __amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw,
