@@ -107,7 +107,9 @@ int kva_layer_pools(const kva_cache *cache, int32_t layer, void **k_pool, void *
  * (engine.py:101-117); here capacity grows a page at a time.               */
 int kva_seq_reserve(kva_cache *cache, int32_t seq_id, int32_t n_tokens);
 /* Give sequence `seq_id` an explicit block list (e.g. a permuted one).  The
- * blocks must be free; the sequence's previous blocks are released.        */
+ * blocks must be free; the sequence's previous blocks are released.  Ends
+ * the current step (the step plan holds block ids), as kva_seq_set_len and
+ * kva_seq_free do: begin a new one before the next hot-path call.          */
 int kva_seq_set_blocks(kva_cache *cache, int32_t seq_id, const int32_t *block_ids,
                        int32_t n_blocks);
 /* Release a sequence's blocks and set its length to 0: KVCache.reset()
@@ -138,9 +140,10 @@ int kva_sync_tables(kva_cache *cache, kva_stream_t stream);
  * len + depth.  tree_bits (nullable, one per new token) gives, for tree
  * verify, the set of new tokens of the same sequence that token sees
  * (bit j = j-th new token of that sequence; self and ancestors).  One
- * host->device copy on `stream` carries the plan and any block-table
- * changes; every layer of the step reuses it (the reference patches the
- * same per-step arguments for all layers: c_dispatch.c:426-456).           */
+ * host->device copy on `stream` carries the plan (with the block ids of
+ * each sequence's first 64 pages) and any block-table changes; every layer
+ * of the step reuses it (the reference patches the same per-step arguments
+ * for all layers: c_dispatch.c:426-456).                                   */
 int kva_step_begin(kva_cache *cache, int32_t n_seqs, const int32_t *seq_ids,
                    const int32_t *n_new, const int32_t *rope_pos,
                    const uint64_t *tree_bits, kva_stream_t stream);

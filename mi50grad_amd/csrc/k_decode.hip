@@ -775,43 +775,78 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     const int b = u / hkv;
     const int h = u - b * hkv;
     const int hq0 = h * (nh / hkv) + z * GP;  // this workgroup's first query head
-    // The length and the cache slot are requested together (no branch on the
-    // length between them); an empty sequence walks nothing and writes no
-    // output.
-    const int ctx = a.ctx_lens ? ld_uniform(a.ctx_lens + b) : a.ctx_len_const;
-    const int sid = a.table ? ld_uniform(a.seq_ids + b) : 0;
-    const int pos = kFused ? ld_uniform(a.app.tok_pos + b) : 0;
-    const int walk = kFused ? ctx - 1 : ctx;  // cached rows the waves walk
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // First round: every request that needs only the kernel arguments (the
+    // plan's page ids, this workgroup's q rows; fused: the new K and V rows
+    // and the norm weights) goes out before the scalar loads of the length,
+    // the sequence id and the position.  A wait for one scalar load waits
+    // for every scalar load in flight, so an argument fetched after those
+    // loads would hold back the requests that need it until they had
+    // arrived.  The first K/V loads then wait for one round trip (the length
+    // and the page ids), not two (the table row needs the sequence id).
+    // Page ids: lane k holds page k's, for the sequence's first 64 pages;
+    // past the 64th they come from the table.
+    static_assert(kPlanPages == 64, "one plan page id per lane");
     const int lane = threadIdx.x & 63;
-    const int r = lane >> 4;
-    const int j = lane & 15;
-    const int row_bytes = hkv * kHeadDim * 2;
-    const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
-    const size_t seq_ofs = a.table ? 0 : static_cast<size_t>(b) * a.seq_stride * 2;
-    const char *kpool = reinterpret_cast<const char *>(a.k_pool) + seq_ofs + h * kHeadDim * 2;
-    const char *vpool = reinterpret_cast<const char *>(a.v_pool) + seq_ofs + h * kHeadDim * 2;
-    // Page ids of the sequence's first 64 pages, lane k holding page k's.
-    const int32_t *row = a.table ? a.table + static_cast<size_t>(sid) * a.table_stride : nullptr;
-    const int npg = (max(ctx, 0) + kBlockTokens - 1) / kBlockTokens;
-    const int ids = (row && lane < npg) ? row[lane] : 0;
-    // The GP query rows (fused: and the new K, V rows with the norm weights
-    // and this position's cos/sin), requested before the first K/V loads.
+    // A buffer load over the sequence's 64 ids (an empty range without a
+    // plan: zeros, no memory touched), so the compiler neither waits on a
+    // branch nor folds it into the table read below.
+    const int32_t *pid_p = a.plan_pages;
+    const auto pid_rs = ro_rsrc(pid_p ? pid_p + static_cast<size_t>(b) * kPlanPages : nullptr,
+                                pid_p ? kPlanPages * 4u : 0u);
+    const int plan_ids = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(pid_rs, 4 * lane, 0, 0));
     const int qi = threadIdx.x;
     const int hw = threadIdx.x >> 5;  // fused: the half-wave's row
     const int l32 = threadIdx.x & 31;
     uint4 qin = make_uint4(0, 0, 0, 0);
-    NormRopeIn nin{};
+    uint4 win = make_uint4(0, 0, 0, 0);
     if constexpr (kFused) {
         const AppendArgs &ap = a.app;
         const uint16_t *src = hw < GP    ? ap.q + (static_cast<size_t>(b) * nh + hq0 + hw) * kHeadDim
                               : hw == GP ? ap.k + (static_cast<size_t>(b) * hkv + h) * kHeadDim
                                          : ap.v + (static_cast<size_t>(b) * hkv + h) * kHeadDim;
         if (hw <= GP + 1) qin = ld16(src + 8 * l32);
-        nin = norm_rope_in<32>(hw < GP ? ap.q_w : ap.k_w, ap.cos_tab + static_cast<size_t>(pos) * ap.half_rot,
-                               ap.sin_tab + static_cast<size_t>(pos) * ap.half_rot, ap.half_rot, l32);
+        win = ld16((hw < GP ? ap.q_w : ap.k_w) + 8 * l32);
     } else {
         if (qi < GP * 32) qin = ld16(a.q + (static_cast<size_t>(b) * nh + hq0) * kHeadDim + 8 * qi);
+    }
+    const int32_t *ctx_p = a.ctx_lens, *sid_p = a.seq_ids, *tab = a.table;
+    const int32_t *pos_p = kFused ? a.app.tok_pos : nullptr;
+    const int half_rot = kFused ? a.app.half_rot : 0;  // addresses this position's cos/sin
+    asm volatile("" ::"s"(ctx_p), "s"(sid_p), "s"(tab), "s"(pos_p), "s"(half_rot));
+    __builtin_amdgcn_sched_barrier(0);
+    // The length, the sequence id and the position are requested together
+    // (no branch on the length between them); an empty sequence walks
+    // nothing and writes no output.
+    const int ctx = ctx_p ? ld_uniform(ctx_p + b) : a.ctx_len_const;
+    const int sid = tab ? ld_uniform(sid_p + b) : 0;
+    const int pos = kFused ? ld_uniform(pos_p + b) : 0;
+    // Taken in here, together: kernel arguments fetched after this point
+    // then wait only for themselves.
+    asm volatile("" ::"s"(ctx), "s"(sid), "s"(pos));
+    __builtin_amdgcn_sched_barrier(0);
+    const int walk = kFused ? ctx - 1 : ctx;  // cached rows the waves walk
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane >> 4;
+    const int j = lane & 15;
+    const int row_bytes = hkv * kHeadDim * 2;
+    const size_t page_bytes = static_cast<size_t>(kBlockTokens) * row_bytes;
+    const size_t seq_ofs = tab ? 0 : static_cast<size_t>(b) * a.seq_stride * 2;
+    const char *kpool = reinterpret_cast<const char *>(a.k_pool) + seq_ofs + h * kHeadDim * 2;
+    const char *vpool = reinterpret_cast<const char *>(a.v_pool) + seq_ofs + h * kHeadDim * 2;
+    // Without the plan's ids (a contiguous cache has none to read), lane k
+    // reads page k's from the table row.
+    const int32_t *row = tab ? tab + static_cast<size_t>(sid) * a.table_stride : nullptr;
+    const int npg = (max(ctx, 0) + kBlockTokens - 1) / kBlockTokens;
+    const int ids = pid_p ? plan_ids : (row && lane < npg) ? row[lane] : 0;
+    // Fused: this position's cos/sin, requested after the position arrives
+    // and waited for only where the rows are normalised (after the first
+    // K/V loads go out).
+    NormRopeIn nin{};
+    if constexpr (kFused) {
+        const AppendArgs &ap = a.app;
+        nin.w = win;
+        rope_in(nin, hw < GP ? ap.q_w : ap.k_w, ap.cos_tab + static_cast<size_t>(pos) * half_rot,
+                ap.sin_tab + static_cast<size_t>(pos) * half_rot, half_rot, l32);
     }
 
     const int n_hp = (max(walk, 0) + kHalf - 1) / kHalf;
@@ -819,12 +854,20 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     const uint32_t koff = r * row_bytes + 16 * j;
     const uint32_t voff = 8 * lane;
     // Issue this wave's i-th half page into p (a no-op load past the list).
+    // Block id of page pg (wave-uniform): the first 64 from the lanes' ids,
+    // later ones from the table row by a vector load, which the compiler
+    // keeps inside its branch (a scalar load it would issue for every page,
+    // and the first K/V loads would wait for it).
+    auto page_of = [&](int pg) -> int {
+        if (!row) return pg;
+        if (pg < 64) return __builtin_amdgcn_readlane(ids, pg);
+        return __builtin_amdgcn_readfirstlane(row[pg]);
+    };
     auto issue = [&](HalfPage &p, int i) {
         const bool on = i < n_i;
         const int hp = on ? wave + kWholeWaves * i : 0;
         const int pg = hp >> 1;
-        int id = pg;
-        if (row) id = pg < 64 ? __builtin_amdgcn_readlane(ids, pg) : ld_uniform(row + pg);
+        const int id = page_of(pg);
         const size_t ofs = static_cast<size_t>(id) * page_bytes + static_cast<size_t>(hp & 1) * kHalf * row_bytes;
         load_half(p, kpool + ofs, vpool + ofs, min(kHalf, walk - hp * kHalf), on, koff, voff, row_bytes);
     };
@@ -849,8 +892,7 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
         // The first head group of (b, h) writes the new rows into slot ctx - 1.
         const int slot = ctx - 1;
         const int pg = max(slot, 0) >> 4;
-        int id = pg;
-        if (row) id = pg < 64 ? __builtin_amdgcn_readlane(ids, pg) : ld_uniform(row + pg);
+        const int id = page_of(pg);
         if (z == 0 && ctx > 0 && (hw == GP || hw == GP + 1)) {
             const size_t at = ((static_cast<size_t>(id) * kBlockTokens + (slot & 15)) * hkv + h) * kHeadDim + 8 * l32;
             st16((hw == GP ? ap.k_pool : ap.v_pool) + at, hw == GP ? y : qin);

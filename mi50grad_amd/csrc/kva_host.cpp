@@ -118,7 +118,7 @@ struct kva_cache {
     size_t off_upre = 0, off_mqpre = 0;
     bool st_all_one = false, st_has_bits = false;
     size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
-           off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0;
+           off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0, off_pids = 0;
 
     // Caller's timing events around the dominant kernel of each hot call
     // (kva_kernel_events); null: none.
@@ -143,7 +143,7 @@ struct kva_graph {
     hipGraphExec_t exec = nullptr;
     int32_t n_seqs = 0, n_tok = 0, table_rows = 0;
     bool all_one = false, has_bits = false;
-    size_t offs[11] = {};
+    size_t offs[12] = {};
 };
 
 namespace {
@@ -341,7 +341,8 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
     c->used.assign(cfg->max_blocks, 0);
     c->free_list.resize(cfg->max_blocks);
     for (int32_t i = 0; i < cfg->max_blocks; ++i) c->free_list[i] = cfg->max_blocks - 1 - i;
-    // Step plan: 5 per-sequence arrays + 3 per-token arrays + bits.
+    // Step plan: 5 per-sequence arrays + 3 per-token arrays + bits + the
+    // first kPlanPages block ids of each sequence.
     // Multi-query units: at most (tokens/Q + sequences) tiles per kv head,
     // Q >= the one-tile token count of the group.
     const size_t q_min = static_cast<size_t>(kva::mq_tile_tokens(cfg->num_heads / cfg->num_kv_heads, 4, 1));
@@ -350,7 +351,8 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
     c->step_bytes = round_up(sizeof(int32_t) * (6 * static_cast<size_t>(cfg->max_seqs) + 3), 256) +
                     round_up(sizeof(int32_t) * (max_units + 1), 256) +
                     round_up(sizeof(int32_t) * 3 * static_cast<size_t>(cfg->max_step_tokens), 256) +
-                    round_up(sizeof(uint64_t) * static_cast<size_t>(cfg->max_step_tokens), 256) + 1024;
+                    round_up(sizeof(uint64_t) * static_cast<size_t>(cfg->max_step_tokens), 256) +
+                    round_up(sizeof(int32_t) * kva::kPlanPages * static_cast<size_t>(cfg->max_seqs), 256) + 1024;
     const size_t patch_cap = std::max<size_t>(4096, cfg->max_seqs + cfg->max_step_tokens);
     c->aux_bytes = round_up(std::max(patch_cap * 3 * sizeof(int32_t),
                                      (static_cast<size_t>(cfg->max_step_tokens) * 3 + cfg->max_seqs + 1) *
@@ -506,6 +508,7 @@ int kva_seq_set_blocks(kva_cache *c, int32_t seq, const int32_t *ids, int32_t n)
     }
     c->nblk[seq] = n;
     c->freed[seq] = 0;
+    c->step_valid = false;  // the step plan holds the old block ids
     return KVA_OK;
 }
 
@@ -660,7 +663,8 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     const size_t o_tslot = round_up(o_tseq + sizeof(int32_t) * n_tok, 16);
     const size_t o_tpos = round_up(o_tslot + sizeof(int32_t) * n_tok, 16);
     const size_t o_bits = round_up(o_tpos + sizeof(int32_t) * n_tok, 16);
-    const size_t total = o_bits + (tree_bits ? sizeof(uint64_t) * n_tok : 0);
+    const size_t o_pids = round_up(o_bits + (tree_bits ? sizeof(uint64_t) * n_tok : 0), 16);
+    const size_t total = o_pids + sizeof(int32_t) * kva::kPlanPages * n_seqs;
 
     std::vector<uint8_t> local;
     uint8_t *h = nullptr;
@@ -702,6 +706,17 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     }
     p_off[n_seqs] = t;
     p_pre[n_seqs] = static_cast<int32_t>(pages);
+    // The block ids of each sequence's first kPlanPages pages (the blocks the
+    // step needs are reserved above), zeros past its pages.
+    int32_t *p_pids = at<int32_t>(h, o_pids);
+    for (int32_t b = 0; b < n_seqs; ++b) {
+        const int32_t np =
+            std::min<int32_t>((p_ctx[b] + kva::kBlockTokens - 1) / kva::kBlockTokens, kva::kPlanPages);
+        const int32_t *row = c->table.data() + static_cast<size_t>(seq_ids[b]) * c->cfg.max_blocks_per_seq;
+        int32_t *dst = p_pids + static_cast<size_t>(b) * kva::kPlanPages;
+        std::copy(row, row + np, dst);
+        std::fill(dst + np, dst + kva::kPlanPages, 0);
+    }
     // Multi-query units in (kv head, sequence, tile) order with their key
     // blocks: a tree tile reads the whole cache, a causal tile reads up to
     // its last token's slot.  upre[b] counts the tiles of earlier sequences
@@ -751,6 +766,7 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->off_tpos = o_tpos;
     c->off_bits = o_bits;
     c->off_pre = o_pre;
+    c->off_pids = o_pids;
     c->st_n_seqs = n_seqs;
     c->st_n_tok = static_cast<int32_t>(n_tok);
     c->st_max_ctx = max_ctx;
@@ -1064,6 +1080,7 @@ static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *g
     a.seq_ids = at<int32_t>(c->d_step, c->off_seq);
     a.ctx_lens = at<int32_t>(c->d_step, c->off_ctx);
     a.pre_seq = at<int32_t>(c->d_step, c->off_pre);
+    a.plan_pages = at<int32_t>(c->d_step, c->off_pids);
     a.n_seqs = c->st_n_seqs;
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
@@ -1468,8 +1485,8 @@ int kva_graph_capture_end(kva_cache *c, kva_stream_t stream, kva_graph **out) {
     g->table_rows = c->cap_table_rows;
     g->all_one = c->st_all_one;
     g->has_bits = c->st_has_bits;
-    const size_t offs[11] = {c->off_seq,  c->off_ctx,  c->off_start, c->off_tokoff, c->off_tseq, c->off_tslot,
-                             c->off_tpos, c->off_bits, c->off_pre,   c->off_upre,   c->off_mqpre};
+    const size_t offs[12] = {c->off_seq,  c->off_ctx,  c->off_start, c->off_tokoff, c->off_tseq,  c->off_tslot,
+                             c->off_tpos, c->off_bits, c->off_pre,   c->off_upre,   c->off_mqpre, c->off_pids};
     std::memcpy(g->offs, offs, sizeof(offs));
     *out = g;
     return KVA_OK;
@@ -1480,8 +1497,8 @@ int kva_graph_launch(kva_graph *g, kva_stream_t stream) {
     kva_cache *c = g->cache;
     if (c->capturing) return fail(KVA_ERR_STATE, "a graph is being recorded");
     if (!c->step_valid) return fail(KVA_ERR_STATE, "no step begun (kva_step_begin)");
-    const size_t offs[11] = {c->off_seq,  c->off_ctx,  c->off_start, c->off_tokoff, c->off_tseq, c->off_tslot,
-                             c->off_tpos, c->off_bits, c->off_pre,   c->off_upre,   c->off_mqpre};
+    const size_t offs[12] = {c->off_seq,  c->off_ctx,  c->off_start, c->off_tokoff, c->off_tseq,  c->off_tslot,
+                             c->off_tpos, c->off_bits, c->off_pre,   c->off_upre,   c->off_mqpre, c->off_pids};
     if (c->st_n_seqs != g->n_seqs || c->st_n_tok != g->n_tok || c->st_all_one != g->all_one ||
         c->st_has_bits != g->has_bits || std::memcmp(offs, g->offs, sizeof(offs)) != 0)
         return fail(KVA_ERR_STATE, "the current step (%d sequences, %d tokens) is not the recorded shape (%d, %d)",

@@ -14,6 +14,7 @@ constexpr int kHeadDim = 256;     // the only head_dim the paged kernels take
 constexpr int kBlockTokens = 16;  // tokens per page
 constexpr int kDecodeHeadsPerWg = 4;  // kv heads per stream-K decode workgroup (one wave each), at most
 constexpr int kSplitQuantum = 16; // decode split sizes are whole pages
+constexpr int kPlanPages = 64;    // page ids per sequence in the step plan (one per lane)
 
 // Fused QK-RMSNorm + RoPE + K/V append over all new tokens of a step.
 struct AppendArgs {
@@ -133,6 +134,12 @@ struct DecodeArgs {
     const int32_t *ctx_lens;  // device [n_seqs] (null: use ctx_len_const)
     const int32_t *pre_seq;   // device [n_seqs+1]: pages of earlier sequences
                               // (null: every sequence has ctx_len_const)
+    // Device [n_seqs][kPlanPages] (null: read the table): the block ids of
+    // each sequence's first kPlanPages pages, copied from the table into the
+    // step plan when the step began (zeros past its pages), so the
+    // whole-sequence form reads them with the length instead of after the
+    // sequence id.
+    const int32_t *plan_pages;
     int32_t ctx_len_const;
     int32_t n_seqs;
     int32_t num_heads;

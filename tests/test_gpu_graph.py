@@ -10,7 +10,9 @@ outputs and, at the end, every pool byte must equal the eager twin's, and
 every replayed output is also compared with the oracle (attention over the
 oracle's own copy of the rows within 2e-3; O-projection within one fp16 ulp
 of ``orc.out_project`` on the replay's own gated rows).  Also: what
-recording refuses, and a replay whose step has another shape.
+recording refuses, a replay whose step has another shape, and a
+whole-sequence recording replayed past 64 pages (block ids beyond the step
+plan's, read from the table).
 """
 import numpy as np
 import pytest
@@ -49,10 +51,26 @@ def test_graph_replay_matches_eager(device, lengths, split, fused):
     the whole-sequence form at the automatic split; append + stream-K decode
     with the split set), recorded and replayed like the two-call form."""
     say(f"graph replay lengths={lengths} split={split} fused={fused}")
+    _replay(device, lengths, split, fused, steps=21, same_outputs=True, other_shape=True)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_graph_whole_form_past_64_pages(device, fused):
+    """A step recorded in the whole-sequence form (longest sequence 1021
+    rows, 64 pages) keeps that form as the replays take the sequences past
+    1024 rows: the walk then reads page 64, whose block id comes from the
+    table rather than the step plan's 64 ids, and (fused) writes the new
+    rows there.  The eager twin runs stream-K past 1024 rows, so replayed
+    outputs are held to the oracle (2e-3) and the pools to the twin's bits."""
+    say(f"graph replay past 64 pages fused={fused}")
+    _replay(device, [1020, 300], 0, fused, steps=12, same_outputs=False, other_shape=False)
+
+
+def _replay(device, lengths, split, fused, steps, same_outputs, other_shape):
     rng = np.random.default_rng(5)
     (eager, graphed), hist = _twin(lengths, split, seed=11)
     B = len(lengths)
-    tables = Tables(device, 512)
+    tables = Tables(device, max(512, max(lengths) + steps + 16))
     stream = Stream()
     h_qw = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float16) for _ in range(LAYERS)]
     h_kw = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float16) for _ in range(LAYERS)]
@@ -89,7 +107,7 @@ def test_graph_replay_matches_eager(device, lengths, split, fused):
             cache.decode(layer, b["q"], b["out"], stream=stream_h)
 
     graph = None
-    for step in range(21):
+    for step in range(steps):
         inputs = [dict(q=fresh((B, H, D)), k=fresh((B, HKV, D)), v=fresh((B, HKV, D))) for _ in range(LAYERS)]
         upload(inputs)
         device.synchronize()
@@ -111,7 +129,8 @@ def test_graph_replay_matches_eager(device, lengths, split, fused):
         for layer in range(LAYERS):
             got = bufs[1][layer]["out"].numpy()
             exp = bufs[0][layer]["out"].numpy()
-            assert np.array_equal(got.view(np.uint16), exp.view(np.uint16)), (step, layer)
+            if same_outputs:
+                assert np.array_equal(got.view(np.uint16), exp.view(np.uint16)), (step, layer)
             assert np.array_equal(bufs[1][layer]["q"].numpy().view(np.uint16),
                                   bufs[0][layer]["q"].numpy().view(np.uint16)), (step, layer)
             qn = expected_norm(inputs[layer]["q"], h_qw[layer], tables, pos)
@@ -127,11 +146,11 @@ def test_graph_replay_matches_eager(device, lengths, split, fused):
         kg, vg = graphed.download_pools(layer)
         assert np.array_equal(ke.view(np.uint16), kg.view(np.uint16))
         assert np.array_equal(ve.view(np.uint16), vg.view(np.uint16))
-    assert [graphed.seq_len(b) for b in range(B)] == [L + 21 for L in lengths]
-    # A step of another shape is refused.
-    graphed.begin_step([0], [1], stream=stream.handle)
-    with pytest.raises(KvaError):
-        graph.launch()
+    assert [graphed.seq_len(b) for b in range(B)] == [L + steps for L in lengths]
+    if other_shape:  # a step of another shape is refused
+        graphed.begin_step([0], [1], stream=stream.handle)
+        with pytest.raises(KvaError):
+            graph.launch()
     graph.destroy()
     stream.synchronize()
     stream.destroy()

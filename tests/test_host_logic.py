@@ -81,6 +81,23 @@ def test_set_blocks_validation():
     assert c.free_block_count() == 18
 
 
+def test_set_blocks_ends_the_step():
+    """The step plan holds the block ids of the step's first pages (the
+    whole-sequence decode reads them with the lengths), so replacing a
+    sequence's blocks ends the step, as setting a length does."""
+    c = make()
+    c.begin_step([0], [1])
+    with pytest.raises(KvaError) as e:
+        c.decode(0, 1 << 20, 1 << 20)
+    assert code(e) == -3                      # past the step check: no device
+    c.set_blocks(1, [5])
+    with pytest.raises(KvaError) as e:
+        c.decode(0, 1 << 20, 1 << 20)
+    assert code(e) == -8                      # no step begun
+    c.begin_step([0, 1], [1, 1])
+    assert c.seq_len(0) == 2 and c.seq_len(1) == 1
+
+
 def test_bad_sequence_ids():
     c = make()
     for s in (-1, 4):
