@@ -15,44 +15,54 @@ namespace {
 // One 32-lane group per row; rows of a token: H query heads, Hkv key heads,
 // Hkv value heads.  8 rows per 256-thread workgroup, all of one token (the
 // launch packs each token's rows into whole workgroups), so the token's
-// position, sequence, slot and page id are workgroup-uniform scalar loads,
-// and the norm weights and cos/sin rows go out with the row's own load.
+// position, sequence, slot and page id are workgroup-uniform scalar loads.
+// Two memory round trips before the stores: first the token's position,
+// sequence and slot with the group's row and norm weights; then cos/sin
+// (at the position) and, in a workgroup holding key or value rows, the page
+// id (at the sequence and slot).  Requested in source order the row waited
+// for the position, and a key or value row's page id for the sequence and
+// slot requested after it: four round trips before a cache store.
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
-    const int rows_per_tok = a.num_heads + 2 * a.num_kv_heads;
+    const int nh = a.num_heads, hkv = a.num_kv_heads;
+    const int rows_per_tok = nh + 2 * hkv;
     const int blocks_per_tok = (rows_per_tok + 7) / 8;
     const int t = blockIdx.x / blocks_per_tok;
-    const int hr = (blockIdx.x - t * blocks_per_tok) * 8 + (threadIdx.x >> 5);
+    const int r0 = (blockIdx.x - t * blocks_per_tok) * 8;
+    const int hr = r0 + (threadIdx.x >> 5);
     const int lane = threadIdx.x & 31;
     if (hr >= rows_per_tok) return;  // whole 32-lane group leaves
-    const int hkv = a.num_kv_heads;
+    const bool is_q = hr < nh, is_k = !is_q && hr < nh + hkv;
+    uint16_t *const x = is_q   ? a.q + (static_cast<size_t>(t) * nh + hr) * kHeadDim
+                        : is_k ? a.k + (static_cast<size_t>(t) * hkv + hr - nh) * kHeadDim
+                               : const_cast<uint16_t *>(a.v) + (static_cast<size_t>(t) * hkv + hr - nh - hkv) * kHeadDim;
+    const uint4 xin = ld16(x + 8 * lane);
+    NormRopeIn nin;
+    nin.w = ld16((is_q ? a.q_w : a.k_w) + 8 * lane);  // unused by a value row
+    const int stride = a.table_stride, keep_k = a.keep_k;
     const int pos = ld_uniform(a.tok_pos + t);
-    const uint16_t *cos_row = a.cos_tab + static_cast<size_t>(pos) * a.half_rot;
-    const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
-
-    if (hr < a.num_heads) {
-        uint16_t *x = a.q + (static_cast<size_t>(t) * a.num_heads + hr) * kHeadDim;
-        const uint4 xin = ld16(x + 8 * lane);
-        const NormRopeIn nin = norm_rope_in<32>(a.q_w, cos_row, sin_row, a.half_rot, lane);
-        st16(x + 8 * lane, norm_rope_apply<32>(xin, nin, a.half_rot, a.eps, lane));
-        return;
-    }
     const int seq = ld_uniform(a.tok_seq + t);
     const int slot = ld_uniform(a.tok_slot + t);
-    const int blk = ld_uniform(a.table + static_cast<size_t>(seq) * a.table_stride + (slot >> 4));
-    const size_t row_base = (static_cast<size_t>(blk) * kBlockTokens + (slot & 15)) * hkv;
-    if (hr < a.num_heads + hkv) {
-        const int kh = hr - a.num_heads;
-        uint16_t *x = a.k + (static_cast<size_t>(t) * hkv + kh) * kHeadDim;
-        const uint4 xin = ld16(x + 8 * lane);
-        const NormRopeIn nin = norm_rope_in<32>(a.k_w, cos_row, sin_row, a.half_rot, lane);
-        const uint4 y = norm_rope_apply<32>(xin, nin, a.half_rot, a.eps, lane);
-        if (!a.keep_k) st16(x + 8 * lane, y);
-        st16(a.k_pool + (row_base + kh) * kHeadDim + 8 * lane, y);
-    } else {
-        const int vh = hr - a.num_heads - hkv;
-        const uint16_t *x = a.v + (static_cast<size_t>(t) * hkv + vh) * kHeadDim;
-        st16(a.v_pool + (row_base + vh) * kHeadDim + 8 * lane, ld16(x + 8 * lane));
+    asm volatile("" ::"s"(pos), "s"(seq), "s"(slot), "s"(stride), "s"(keep_k));  // taken in together
+    __builtin_amdgcn_sched_barrier(0);
+    // Second round: cos/sin (branch-free, so nothing waits for them before
+    // the page id goes out; a value row's are unused) and the page id.
+    rope_in_flat(nin, a.k_w, a.cos_tab + static_cast<size_t>(pos) * a.half_rot,
+                 a.sin_tab + static_cast<size_t>(pos) * a.half_rot, a.half_rot, lane);
+    const bool any_kv = r0 + 7 >= nh;  // workgroup-uniform
+    const int blk = any_kv ? ld_uniform(a.table + static_cast<size_t>(seq) * stride + (slot >> 4)) : 0;
+    if (!is_q && !is_k) {
+        const size_t row_base = (static_cast<size_t>(blk) * kBlockTokens + (slot & 15)) * hkv;
+        st16(a.v_pool + (row_base + hr - nh - hkv) * kHeadDim + 8 * lane, xin);
+        return;
     }
+    const uint4 y = norm_rope_apply<32>(xin, nin, a.half_rot, a.eps, lane);
+    if (is_q) {
+        st16(x + 8 * lane, y);
+        return;
+    }
+    const size_t row_base = (static_cast<size_t>(blk) * kBlockTokens + (slot & 15)) * hkv;
+    if (!keep_k) st16(x + 8 * lane, y);
+    st16(a.k_pool + (row_base + hr - nh) * kHeadDim + 8 * lane, y);
 }
 
 template <int LANES>

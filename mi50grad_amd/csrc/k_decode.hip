@@ -845,8 +845,8 @@ __global__ __launch_bounds__(64 * kWholeWaves) void whole_kernel(DecodeArgs a) {
     if constexpr (kFused) {
         const AppendArgs &ap = a.app;
         nin.w = win;
-        rope_in(nin, hw < GP ? ap.q_w : ap.k_w, ap.cos_tab + static_cast<size_t>(pos) * half_rot,
-                ap.sin_tab + static_cast<size_t>(pos) * half_rot, half_rot, l32);
+        rope_in_flat(nin, hw < GP ? ap.q_w : ap.k_w, ap.cos_tab + static_cast<size_t>(pos) * half_rot,
+                     ap.sin_tab + static_cast<size_t>(pos) * half_rot, half_rot, l32);
     }
 
     const int n_hp = (max(walk, 0) + kHalf - 1) / kHalf;

@@ -22,6 +22,20 @@ struct NormRopeIn {
     uint2 c, s;
 };
 
+// The cos/sin half of norm_rope_in, for a caller that requests the weights
+// earlier.
+__device__ __forceinline__ void rope_in(NormRopeIn &in, const uint16_t *__restrict__ cos_row,
+                                        const uint16_t *__restrict__ sin_row, int half_rot, int lane) {
+    if (half_rot > 0) {
+        const int cl = min(lane, half_rot / 4 - 1);
+        in.c = ld8(cos_row + 4 * cl);
+        in.s = ld8(sin_row + 4 * cl);
+    } else {
+        in.c = make_uint2(0, 0);
+        in.s = make_uint2(0, 0);
+    }
+}
+
 // Lanes past LANES get zero weights; lanes past the rotary pairs read the
 // last lane's cos/sin (in bounds, never used).  half_rot % 4 == 0.
 template <int LANES>
@@ -31,26 +45,18 @@ __device__ __forceinline__ NormRopeIn norm_rope_in(const uint16_t *__restrict__ 
                                                    int lane) {
     NormRopeIn in;
     in.w = (lane < LANES) ? ld16(w + 8 * lane) : make_uint4(0, 0, 0, 0);
-    if (half_rot > 0) {
-        const int cl = min(lane, half_rot / 4 - 1);
-        in.c = ld8(cos_row + 4 * cl);
-        in.s = ld8(sin_row + 4 * cl);
-    } else {
-        in.c = make_uint2(0, 0);
-        in.s = make_uint2(0, 0);
-    }
+    rope_in(in, cos_row, sin_row, half_rot, lane);
     return in;
 }
 
-// The cos/sin half of norm_rope_in without its branch, for a caller that
-// requests the weights earlier and must not wait for cos/sin before its
-// next requests (a merge of loaded values after the branch makes the
-// compiler wait for them there).  With no rotary part the loads read the
+// rope_in without its branch, for a caller that must not wait for cos/sin
+// before its next requests (a merge of loaded values after the branch makes
+// the compiler wait for them there).  With no rotary part the loads read the
 // weight row w instead (in bounds; norm_rope_apply uses c and s only on
 // lanes that hold rotary pairs).
-__device__ __forceinline__ void rope_in(NormRopeIn &in, const uint16_t *__restrict__ w,
-                                        const uint16_t *__restrict__ cos_row, const uint16_t *__restrict__ sin_row,
-                                        int half_rot, int lane) {
+__device__ __forceinline__ void rope_in_flat(NormRopeIn &in, const uint16_t *__restrict__ w,
+                                             const uint16_t *__restrict__ cos_row,
+                                             const uint16_t *__restrict__ sin_row, int half_rot, int lane) {
     const bool rot = half_rot > 0;
     const int cl = rot ? min(lane, half_rot / 4 - 1) : 0;
     in.c = ld8((rot ? cos_row : w) + 4 * cl);
