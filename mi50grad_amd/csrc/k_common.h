@@ -90,6 +90,16 @@ __device__ __forceinline__ float wave_groups_sum(float x) {
 // through the scalar cache: a load in the constant address space with a
 // uniform address becomes a scalar load, counted apart from the vector
 // loads, so waiting for it does not also wait for K/V data in flight.
+// floor(a * b / d) for 0 <= a, b and d > 0 (a stream-K share boundary): in
+// 32 bits when the product fits, as it does for any realistic step (a 64-bit
+// division is several times the instructions, and the combine kernels wait
+// on these before their first loads); exact either way.
+__device__ __forceinline__ int floor_muldiv(int a, int b, int d) {
+    const uint64_t x = static_cast<uint64_t>(a) * static_cast<uint32_t>(b);
+    return static_cast<int>(x <= 0xffffffffull ? static_cast<uint32_t>(x) / static_cast<uint32_t>(d)
+                                               : x / static_cast<uint32_t>(d));
+}
+
 __device__ __forceinline__ int32_t ld_uniform(const int32_t *p) {
     return *reinterpret_cast<const __attribute__((address_space(4))) int32_t *>(
         reinterpret_cast<uintptr_t>(p));

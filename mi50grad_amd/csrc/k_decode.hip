@@ -226,14 +226,20 @@ __device__ __forceinline__ const uint16_t *gate_of(const DecodeArgs &a, int b, i
 }
 
 // First page of workgroup w when P pages are shared by W workgroups.
+// kFast: floor_muldiv's 32-bit division when the product fits, for the
+// combine, which waits on these before its first loads; the decode kernel
+// keeps the 64-bit form (the extra branch cost it registers: one wave per
+// SIMD instead of two, C3 114 -> 144 us).
+template <bool kFast = false>
 __device__ __forceinline__ int wg_start(int w, int P, int W) {
-    return static_cast<int>(static_cast<int64_t>(w) * P / W);
+    return kFast ? floor_muldiv(w, P, W) : static_cast<int>(static_cast<int64_t>(w) * P / W);
 }
 
 // The workgroup whose page range holds page p.
+template <bool kFast = false>
 __device__ __forceinline__ int wg_of_page(int p, int P, int W) {
-    int w = static_cast<int>(static_cast<int64_t>(p) * W / P);
-    while (w + 1 < W && wg_start(w + 1, P, W) <= p) ++w;
+    int w = kFast ? floor_muldiv(p, W, P) : static_cast<int>(static_cast<int64_t>(p) * W / P);
+    while (w + 1 < W && wg_start<kFast>(w + 1, P, W) <= p) ++w;
     return w;
 }
 
@@ -629,13 +635,16 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void decode_mfma_kernel(DecodeArgs
 // workgroup costs an L2 writeback per workgroup on multi-XCD parts.  The
 // (m, l) pairs and acc rows of up to kChunk partials are all requested before
 // any is used, so a sequence cut into at most kChunk pieces costs two memory
-// round trips (its length, then its partials), taken by wave 0 alone.  A
-// sequence cut into more pieces (one long sequence over every CU) has its
-// chunks dealt to the kCombineWaves waves, which merge through LDS.
+// round trips (its length, then its partials), taken by wave 0 alone; when
+// the host can show that no sequence of the launch has more pieces, the
+// launch has one wave per workgroup (the other three would only start and
+// leave).  A sequence cut into more pieces (one long sequence over every
+// CU) has its chunks dealt to the waves, which merge through LDS; with one
+// wave, it takes them all in turn.
 constexpr int kCombineWaves = 4;
 template <int G>
 __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs a) {
-    constexpr int kChunk = 16;
+    constexpr int kChunk = kCombineChunk;
     __shared__ float4 w_acc[kCombineWaves * 64];
     __shared__ float w_ml[kCombineWaves * 2];
     const int u = blockIdx.x;
@@ -651,24 +660,27 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs 
     const int npg = (ctx + 15) >> 4;
     if (npg == 0) return;
     const int first = seq_page_base(a, b, npg);
-    const int w0 = wg_of_page(first, P, W);
-    const int w1 = wg_of_page(first + npg - 1, P, W);
+    const int w0 = wg_of_page<true>(first, P, W);
+    const int w1 = wg_of_page<true>(first + npg - 1, P, W);
     if (w0 == w1) return;  // one workgroup covered the sequence and wrote it
     const int n = w1 - w0 + 1;
-    const bool multi = n > kChunk;  // uniform over the workgroup
+    const int nw = blockDim.x >> 6;  // 1 when the host knows no sequence has more than kChunk pieces
+    const bool multi = n > kChunk;   // uniform over the workgroup
     if (!multi && wave != 0) return;
     // Partial i comes from workgroup w0 + i: slot 2w when the sequence began
-    // at or before that workgroup's range, else 2w+1.
+    // at or before that workgroup's range, else 2w+1.  Only w0's range can
+    // begin after the sequence's first page, so one division settles every
+    // slot (one per piece kept the pieces' loads from going out together).
+    const int slot0 = 2 * w0 + (first <= wg_start<true>(w0, P, W) ? 0 : 1);
     auto row_of = [&](int i) -> size_t {
-        const int w = w0 + i;
-        const int slot = 2 * w + (first <= wg_start(w, P, W) ? 0 : 1);
+        const int slot = i == 0 ? slot0 : 2 * (w0 + i);
         return (static_cast<size_t>(slot) * hkv + h) * G + g;
     };
     // Running merge over this wave's chunks: (big, lt, at) is the merge of
     // the chunks so far (big = -inf, lt = 0 before any).
     float big = -INFINITY, lt = 0.0f;
     float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int step = multi ? kCombineWaves * kChunk : kChunk;
+    const int step = multi ? nw * kChunk : kChunk;
     for (int c0 = (multi ? wave : 0) * kChunk; c0 < n; c0 += step) {
         const int cnt = min(kChunk, n - c0);
         float2 ml = make_float2(-INFINITY, 0.0f);
@@ -703,9 +715,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs 
         }
         big = nb;
     }
-    if (multi) {
-        // Wave 0 always holds a chunk; a wave without one (fewer than
-        // kCombineWaves chunks) keeps big = -inf and weighs 0.
+    if (multi && nw > 1) {
+        // Wave 0 always holds a chunk; a wave without one (fewer than nw
+        // chunks) keeps big = -inf and weighs 0.
         w_acc[wave * 64 + lane] = at;
         if (lane == 0) {
             w_ml[wave * 2] = big;
@@ -715,11 +727,13 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs 
         if (wave != 0) return;
         float mm = -INFINITY;
 #pragma unroll
-        for (int v = 0; v < kCombineWaves; ++v) mm = fmaxf(mm, w_ml[v * 2]);
+        for (int v = 0; v < kCombineWaves; ++v)
+            if (v < nw) mm = fmaxf(mm, w_ml[v * 2]);
         lt = 0.0f;
         at = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int v = 0; v < kCombineWaves; ++v) {
+            if (v >= nw) break;
             const float c = __builtin_amdgcn_exp2f(w_ml[v * 2] - mm);  // 0 for a wave without chunks
             const float4 x = w_acc[v * 64 + lane];
             lt += w_ml[v * 2 + 1] * c;
@@ -1032,7 +1046,8 @@ hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(decode_mfma_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(64 * hpw), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess || (e = mark(a.ev_after, s)) != hipSuccess) return e;
-    hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * kCombineWaves), 0, s, a);
+    const int cw = a.combine_waves == 1 ? 1 : kCombineWaves;
+    hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * cw), 0, s, a);
     return hipGetLastError();
 }
 

@@ -56,11 +56,9 @@ template <int KEYS> constexpr int tile_bytes() { return KEYS / 2 * kPairBytes; }
 constexpr float kLog2e = 1.4426950408889634f;
 
 
-__device__ __forceinline__ int mq_wg_start(int w, int n, int W) {
-    return static_cast<int>(static_cast<int64_t>(w) * n / W);
-}
+__device__ __forceinline__ int mq_wg_start(int w, int n, int W) { return floor_muldiv(w, n, W); }
 __device__ __forceinline__ int mq_wg_of(int p, int n, int W) {
-    int w = static_cast<int>(static_cast<int64_t>(p) * W / n);
+    int w = floor_muldiv(p, W, n);
     while (w + 1 < W && mq_wg_start(w + 1, n, W) <= p) ++w;
     return w;
 }
@@ -495,6 +493,10 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     const int w0 = mq_wg_of(ub, NB, W);
     const int w1 = mq_wg_of(ue - 1, NB, W);
     if (w0 == w1) return;  // written whole by one workgroup
+    // Piece ww's slot: 2ww when the unit began at or before that share, else
+    // 2ww+1; only share w0 can begin after the unit's first block, so one
+    // division settles every slot.
+    const int slot0 = 2 * w0 + (ub <= mq_wg_start(w0, NB, W) ? 0 : 1);
     const int hkv = a.num_kv_heads;
     const int G = a.num_heads / hkv;
     const int Q = a.q_tile;
@@ -519,7 +521,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
         for (int i = 0; i < kMaxP; ++i) {
             const int ww = wb + i;
             if (ww <= w1) {
-                const int slot = 2 * ww + (ub <= mq_wg_start(ww, NB, W) ? 0 : 1);
+                const int slot = ww == w0 ? slot0 : 2 * ww;
                 const size_t rowi = static_cast<size_t>(slot) * kMqSlotRows + rho;
                 ml[i] = *reinterpret_cast<const float2 *>(a.ws_ml + rowi * 2);
                 const float4 *src = reinterpret_cast<const float4 *>(a.ws_acc + rowi * kHeadDim + d0);

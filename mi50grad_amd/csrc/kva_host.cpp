@@ -1008,6 +1008,15 @@ int kva_get_decode_split(const kva_cache *c, int32_t *split_tokens, int32_t *n_s
 }
 
 // Fill the stream-K fields of a decode launch over `pages` pages.
+// One wave per combine workgroup when no sequence can be cut into more than
+// kCombineChunk pieces (the combine's other waves only share the chunks of a
+// sequence cut into more): npg pages meet at most floor(npg * W / P) + 2 of
+// W shares of P pages.
+static int32_t combine_waves_for(int64_t max_npg, int64_t pages, int32_t n_wg) {
+    if (pages <= 0) return 4;
+    return max_npg * n_wg / pages + 2 <= kva::kCombineChunk ? 1 : 4;
+}
+
 static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_t num_heads) {
     a.total_pages = static_cast<int32_t>(pages);
     // Two partial slots of num_heads rows per workgroup must fit the workspace.
@@ -1095,9 +1104,12 @@ static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *g
         const int64_t fit = static_cast<int64_t>(c->ws_rows / (2 * static_cast<size_t>(c->cfg.num_heads)));
         const int64_t cap = c->split_user > 0 ? c->max_wg : static_cast<int64_t>(c->n_cu) * kDecodeWgPerCu;
         a.n_wg = static_cast<int32_t>(std::max<int64_t>(1, std::min(cap, fit)));
-        a.dyn = 1;
+        a.dyn = 1;  // the shape is derived at replay, so the combine keeps four waves
         a.split_tokens = c->split_user;
         a.min_pages = kMinPagesPerWg;
+    } else {
+        a.combine_waves = combine_waves_for((c->st_max_ctx + kva::kBlockTokens - 1) / kva::kBlockTokens,
+                                            a.total_pages, a.n_wg);
     }
     a.out = static_cast<uint16_t *>(out);
     a.ev_before = c->kev_before;
@@ -1621,6 +1633,7 @@ static int legacy_decode(kva_cache *ws, const void *q, const void *gate, const v
     } else {
         set_stream_k(ws, a, pages, num_heads);
     }
+    if (!a.whole) a.combine_waves = combine_waves_for(unit_pages, pages, a.n_wg);
     a.out = static_cast<uint16_t *>(out);
     KVA_HIP(kva::launch_decode(a, static_cast<hipStream_t>(stream)));
     return KVA_OK;

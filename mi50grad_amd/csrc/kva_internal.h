@@ -15,6 +15,7 @@ constexpr int kBlockTokens = 16;  // tokens per page
 constexpr int kDecodeHeadsPerWg = 4;  // kv heads per stream-K decode workgroup (one wave each), at most
 constexpr int kSplitQuantum = 16; // decode split sizes are whole pages
 constexpr int kPlanPages = 64;    // page ids per sequence in the step plan (one per lane)
+constexpr int kCombineChunk = 16; // decode partials a combine wave requests together
 
 // Fused QK-RMSNorm + RoPE + K/V append over all new tokens of a step.
 struct AppendArgs {
@@ -152,6 +153,9 @@ struct DecodeArgs {
     int32_t dyn;
     int32_t split_tokens;     // 0 = one workgroup per CU up to the cap
     int32_t min_pages;
+    // 1: the combine launch gets one wave per workgroup (the host has shown
+    // that no sequence is cut into more than kCombineChunk pieces); else four.
+    int32_t combine_waves;
     float *ws_acc;            // [2*n_wg][Hkv][G][256] partial slots
     float *ws_ml;             // [2*n_wg][Hkv][G][2]
     uint16_t *out;            // [n_seqs][H][256]
