@@ -307,35 +307,42 @@ __global__ __launch_bounds__(256) void proj_finish_kernel(ProjectArgs a) {
     const int lane = threadIdx.x & 31;
     if (hr >= rows_per_tok) return;  // whole 32-lane group leaves
     const int t = a.tok0 + tc;
+    // Two memory round trips before the stores.  First: every split's
+    // partial (splits past a.splits reread split 0 and are not added) and
+    // the norm weights, which need only the kernel arguments, with the
+    // token's position, sequence and slot; then cos/sin and the page id.
+    // (Requested in source order, the partials waited for the page id, which
+    // waited for the sequence and slot: three round trips.)
+    const size_t N = static_cast<size_t>(a.n_a) + a.n_b;
+    const size_t row_at = static_cast<size_t>(tc) * N + static_cast<size_t>(hr) * kHeadDim + 8 * lane;
+    const size_t split_stride = static_cast<size_t>(a.n_tok) * N;
+    const int splits = a.splits;
+    float4_t plo[kProjMaxSplits], phi[kProjMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kProjMaxSplits; ++s) {
+        const float *ps = a.part + row_at + (s < splits ? s : 0) * split_stride;
+        plo[s] = *reinterpret_cast<const float4_t *>(ps);
+        phi[s] = *reinterpret_cast<const float4_t *>(ps + 4);
+    }
+    const uint16_t *w = hr < H ? a.q_w : a.k_w;  // gate and value rows load and ignore them
+    NormRopeIn nin;
+    nin.w = ld16(w + 8 * lane);
+    const int stride = a.table_stride, half_rot = a.half_rot;
     const int pos = ld_uniform(a.tok_pos + t);
     const int seq = ld_uniform(a.tok_seq + t);
     const int slot = ld_uniform(a.tok_slot + t);
-    const int blk = ld_uniform(a.table + static_cast<size_t>(seq) * a.table_stride + (slot >> 4));
-    // The norm weights and cos/sin rows go out with the partials, before
-    // anything waits (gate and value rows load and ignore them).
-    const uint16_t *cos_row = a.cos_tab + static_cast<size_t>(pos) * a.half_rot;
-    const uint16_t *sin_row = a.sin_tab + static_cast<size_t>(pos) * a.half_rot;
-    const NormRopeIn nin = norm_rope_in<32>(hr < H ? a.q_w : a.k_w, cos_row, sin_row, a.half_rot, lane);
-    // Every split's partial is loaded at once (splits past a.splits reread
-    // split 0 and are not added), then summed in split order.
-    const size_t N = static_cast<size_t>(a.n_a) + a.n_b;
-    const size_t row_at = static_cast<size_t>(tc) * N + static_cast<size_t>(hr) * kHeadDim + 8 * lane;
+    asm volatile("" ::"s"(pos), "s"(seq), "s"(slot), "s"(stride), "s"(half_rot));  // taken in together
+    __builtin_amdgcn_sched_barrier(0);
+    rope_in_flat(nin, w, a.cos_tab + static_cast<size_t>(pos) * half_rot, a.sin_tab + static_cast<size_t>(pos) * half_rot,
+                 half_rot, lane);
+    const int blk = ld_uniform(a.table + static_cast<size_t>(seq) * stride + (slot >> 4));
     uint4 y;
     {
-        const size_t split_stride = static_cast<size_t>(a.n_tok) * N;
-        const float *p = a.part + row_at;
-        float4_t plo[kProjMaxSplits], phi[kProjMaxSplits];
-#pragma unroll
-        for (int s = 0; s < kProjMaxSplits; ++s) {
-            const float *ps = p + (s < a.splits ? s : 0) * split_stride;
-            plo[s] = *reinterpret_cast<const float4_t *>(ps);
-            phi[s] = *reinterpret_cast<const float4_t *>(ps + 4);
-        }
         float4_t lo = plo[0], hi = phi[0];
 #pragma unroll
         for (int s = 1; s < kProjMaxSplits; ++s) {
-            lo = s < a.splits ? lo + plo[s] : lo;
-            hi = s < a.splits ? hi + phi[s] : hi;
+            lo = s < splits ? lo + plo[s] : lo;
+            hi = s < splits ? hi + phi[s] : hi;
         }
         y.x = pack_h2(lo[0], lo[1]);
         y.y = pack_h2(lo[2], lo[3]);
