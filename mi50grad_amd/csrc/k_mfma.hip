@@ -463,52 +463,28 @@ __global__ __launch_bounds__(64 * WAVES) void mq_kernel(MultiQueryArgs a) {
 }
 
 // Merge the partials of units cut across workgroups: one workgroup per
-// (unit, 16 rows of the tile); thread = (row, 16-dim slice).  Three memory
-// round trips: the unit's block range together with the search for its
-// sequence (a ballot over the unit prefix sums, no dependent loads), then
-// the sequence's token range, then every piece's (m, l) and acc slice,
-// requested before any is used and merged online.
+// (cut unit, 16 rows of its tile); thread = (row, 16-dim slice).  The step
+// plan holds a record per cut unit (kva_step_begin finds them from the same
+// shares as the launch), so a workgroup waits for two memory round trips:
+// its record, then every piece's (m, l) and acc slice, requested before any
+// is used and merged online.  (Found here, from the unit positions, the
+// tile's sequence and token range, the pieces took four, and the launch
+// held a row of workgroups for every unit, cut or not.)
 __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
     constexpr int kMaxP = 4;  // pieces requested together
-    const int u = blockIdx.x;
-    const int lane = threadIdx.x & 63;
-    const int ub = a.mq_pre[u] + mq_unit_cost(a.keys);  // the unit's first block
-    const int ue = a.mq_pre[u + 1];
-    // Head and tile index of unit u (head-major units), and its sequence:
-    // the number of sequences whose tiles end at or before the tile.
-    const int U1 = a.upre[a.n_seqs];
-    const int h = u / U1;
-    const int r = u - h * U1;
-    int b = 0;
-    for (int c0 = 0; c0 < a.n_seqs; c0 += 64) {
-        const int i = c0 + lane;
-        const uint64_t m = __ballot(i < a.n_seqs && a.upre[i + 1] <= r);
-        b += __popcll(m);
-        if (m != ~0ull) break;
-    }
-    b = __builtin_amdgcn_readfirstlane(b);
-    if (ue <= ub) return;
-    const int W = a.n_wg;
-    const int NB = a.total_blocks;
-    const int w0 = mq_wg_of(ub, NB, W);
-    const int w1 = mq_wg_of(ue - 1, NB, W);
-    if (w0 == w1) return;  // written whole by one workgroup
-    // Piece ww's slot: 2ww when the unit began at or before that share, else
-    // 2ww+1; only share w0 can begin after the unit's first block, so one
-    // division settles every slot.
-    const int slot0 = 2 * w0 + (ub <= mq_wg_start(w0, NB, W) ? 0 : 1);
-    const int hkv = a.num_kv_heads;
-    const int G = a.num_heads / hkv;
-    const int Q = a.q_tile;
-    const int tile = r - a.upre[b];
+    const int32_t *rec = a.mq_cut + static_cast<size_t>(blockIdx.x) * kMqCutWords;
+    const int h = ld_uniform(rec);
+    const int tq0 = ld_uniform(rec + 1);      // the tile's first new token (step order)
+    const int n_valid = ld_uniform(rec + 2);  // its tokens
+    const int w0 = ld_uniform(rec + 3);
+    const int w1 = ld_uniform(rec + 4);
+    const int slot0 = ld_uniform(rec + 5);
+    const int G = a.num_heads / a.num_kv_heads;
     const int rho = 16 * blockIdx.y + (threadIdx.x >> 4);
     const int d0 = (threadIdx.x & 15) * 16;
     const int iq = rho / G;
     const int gq = rho - iq * G;
-    const int tok = a.tok_off[b];
-    const int T = a.tok_off[b + 1] - tok;
-    const int qi = tile * Q + iq;
-    if (iq >= Q || qi >= T) return;
+    if (iq >= n_valid) return;
     // Running merge: (big, lt, o) over the pieces so far; m in log2 units.
     float big = -INFINITY, lt = 0.0f;
     float o[16];
@@ -556,7 +532,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(MultiQueryArgs a) {
         big = nb;
     }
     const float inv = 1.0f / lt;
-    const size_t tq = static_cast<size_t>(tok + qi);
+    const size_t tq = static_cast<size_t>(tq0 + iq);
     uint16_t *orow = a.out + (tq * a.num_heads + h * G + gq) * kHeadDim + d0;
     const uint16_t *grow = a.gate ? a.gate + tq * a.gate_stride + (h * G + gq) * kHeadDim + d0 : nullptr;
     uint2 p[4];
@@ -588,7 +564,7 @@ hipError_t launch_mq(const MultiQueryArgs &a, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (a.ev_after && (e = hipEventRecord(a.ev_after, s)) != hipSuccess) return e;
-    hipLaunchKernelGGL(mq_combine_kernel, dim3(a.n_units, WAVES * NT), dim3(256), 0, s, a);
+    if (a.n_cut > 0) hipLaunchKernelGGL(mq_combine_kernel, dim3(a.n_cut, WAVES * NT), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

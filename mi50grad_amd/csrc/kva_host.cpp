@@ -111,6 +111,8 @@ struct kva_cache {
     int32_t st_n_seqs = 0, st_n_tok = 0, st_max_ctx = 0, st_max_new = 0, st_max_pos = 0;
     int32_t st_total_pages = 0;  // pages of all sequences of the step
     int32_t st_mq_units = 0;     // (sequence, token tile, kv head) units
+    int32_t st_mq_wg = 0;        // workgroups of the step's multi-query launch
+    int32_t st_mq_cut = 0;       // its units cut across workgroups (records at off_cut)
     int32_t st_mq_blocks = 0;    // key blocks (and unit start costs) of all multi-query units
     int32_t st_mq_waves = 4;     // waves per workgroup of the multi-query kernel
     int32_t st_mq_keys = 32;     // keys per multi-query block (mq_keys_for)
@@ -118,7 +120,7 @@ struct kva_cache {
     size_t off_upre = 0, off_mqpre = 0;
     bool st_all_one = false, st_has_bits = false;
     size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
-           off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0, off_pids = 0;
+           off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0, off_pids = 0, off_cut = 0;
 
     // Caller's timing events around the dominant kernel of each hot call
     // (kva_kernel_events); null: none.
@@ -352,7 +354,8 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
                     round_up(sizeof(int32_t) * (max_units + 1), 256) +
                     round_up(sizeof(int32_t) * 3 * static_cast<size_t>(cfg->max_step_tokens), 256) +
                     round_up(sizeof(uint64_t) * static_cast<size_t>(cfg->max_step_tokens), 256) +
-                    round_up(sizeof(int32_t) * kva::kPlanPages * static_cast<size_t>(cfg->max_seqs), 256) + 1024;
+                    round_up(sizeof(int32_t) * kva::kPlanPages * static_cast<size_t>(cfg->max_seqs), 256) +
+                    round_up(sizeof(int32_t) * kva::kMqCutWords * max_units, 256) + 1024;
     const size_t patch_cap = std::max<size_t>(4096, cfg->max_seqs + cfg->max_step_tokens);
     c->aux_bytes = round_up(std::max(patch_cap * 3 * sizeof(int32_t),
                                      (static_cast<size_t>(cfg->max_step_tokens) * 3 + cfg->max_seqs + 1) *
@@ -365,6 +368,7 @@ int kva_create(const kva_config *cfg, kva_cache **out) {
     c->proj_floats = static_cast<size_t>(kva::kProjMaxSplits) * kva::kProjTokens *
                      (2 * static_cast<size_t>(cfg->num_heads) + 2 * cfg->num_kv_heads) * kva::kHeadDim;
     c->n_cu = kHostOnlyCus;
+    c->mq_max_wg = c->n_cu;  // the device's CU count below
     if (!c->host_only) {
         auto cleanup = [&](int code) {
             kva_destroy(c);
@@ -664,13 +668,16 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     const size_t o_tpos = round_up(o_tslot + sizeof(int32_t) * n_tok, 16);
     const size_t o_bits = round_up(o_tpos + sizeof(int32_t) * n_tok, 16);
     const size_t o_pids = round_up(o_bits + (tree_bits ? sizeof(uint64_t) * n_tok : 0), 16);
-    const size_t total = o_pids + sizeof(int32_t) * kva::kPlanPages * n_seqs;
+    const size_t o_cut = round_up(o_pids + sizeof(int32_t) * kva::kPlanPages * n_seqs, 16);
+    // The cut-unit records (below) take at most one per unit; only those
+    // written are uploaded.
+    const size_t total_max = o_cut + sizeof(int32_t) * kva::kMqCutWords * n_units;
 
     std::vector<uint8_t> local;
     uint8_t *h = nullptr;
     int idx = -1;
     if (c->host_only) {
-        local.resize(total + 16);
+        local.resize(total_max + 16);
         h = local.data();
     } else {
         int rc = acquire_stage(c, &h, &idx);
@@ -747,6 +754,50 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     }
     p_mqpre[units] = static_cast<int32_t>(blocks);
     if (tree_bits) std::memcpy(h + o_bits, tree_bits, sizeof(uint64_t) * n_tok);
+    // The units the multi-query launch will cut across workgroups (the same
+    // shares: kva::mq_wg_count workgroups over the unit positions), one
+    // record each for its combine: head, the tile's first new token, its
+    // valid tokens, first and last share, and the first piece's slot (2w
+    // when the unit begins at or before share w's start, else 2w+1; every
+    // later share starts inside the unit, so its slot is 2w).
+    const int32_t mq_wg = kva::mq_wg_count(blocks, mq_keys, c->mq_max_wg);
+    // The share holding position p, for non-decreasing p (a cursor: one
+    // division per share boundary passed, so large decode-only steps, which
+    // build the records too, stay cheap).
+    int32_t cur_w = 0;
+    int64_t cur_next = mq_wg > 1 ? kva::mq_share_start(1, blocks, mq_wg) : blocks;
+    auto share_of = [&](int64_t p) {
+        while (cur_w + 1 < mq_wg && cur_next <= p) {
+            ++cur_w;
+            cur_next = kva::mq_share_start(cur_w + 1, blocks, mq_wg);
+        }
+        return cur_w;
+    };
+    int32_t *p_cut = at<int32_t>(h, o_cut);
+    int32_t n_cut = 0;
+    {
+        int64_t u = 0;
+        for (int32_t hh = 0; hh < c->cfg.num_kv_heads; ++hh) {
+            for (int32_t b = 0; b < n_seqs; ++b) {
+                const int32_t tiles = (n_new[b] + mq_q - 1) / mq_q;
+                for (int32_t tl = 0; tl < tiles; ++tl, ++u) {
+                    const int64_t ub = p_mqpre[u] + unit_cost, ue = p_mqpre[u + 1];
+                    if (ue <= ub) continue;
+                    const int32_t w0 = share_of(ub), w1 = share_of(ue - 1);
+                    if (w0 == w1) continue;
+                    int32_t *r = p_cut + static_cast<size_t>(n_cut++) * kva::kMqCutWords;
+                    r[0] = hh;
+                    r[1] = p_off[b] + tl * mq_q;
+                    r[2] = std::min(mq_q, n_new[b] - tl * mq_q);
+                    r[3] = w0;
+                    r[4] = w1;
+                    r[5] = 2 * w0 + (ub <= kva::mq_share_start(w0, blocks, mq_wg) ? 0 : 1);
+                    r[6] = r[7] = 0;
+                }
+            }
+        }
+    }
+    const size_t total = o_cut + sizeof(int32_t) * kva::kMqCutWords * n_cut;
 
     if (!c->host_only) {
         hipStream_t s = static_cast<hipStream_t>(stream);
@@ -767,6 +818,9 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->off_bits = o_bits;
     c->off_pre = o_pre;
     c->off_pids = o_pids;
+    c->off_cut = o_cut;
+    c->st_mq_wg = mq_wg;
+    c->st_mq_cut = n_cut;
     c->st_n_seqs = n_seqs;
     c->st_n_tok = static_cast<int32_t>(n_tok);
     c->st_max_ctx = max_ctx;
@@ -1297,10 +1351,11 @@ static int multi_query(kva_cache *c, int32_t layer, const void *q, void *out, kv
     a.n_units = c->st_mq_units;
     a.total_blocks = c->st_mq_blocks;
     a.keys = c->st_mq_keys;
-    // Stream-K share: one workgroup per CU, at least 128 keys' blocks each.
-    const int64_t min_blocks = 128 / c->st_mq_keys;
-    a.n_wg = static_cast<int32_t>(std::max<int64_t>(
-        1, std::min<int64_t>(c->mq_max_wg, (c->st_mq_blocks + min_blocks - 1) / min_blocks)));
+    // Stream-K share: one workgroup per CU, at least 128 keys' blocks each
+    // (kva::mq_wg_count, as kva_step_begin found the cut units from it).
+    a.n_wg = c->st_mq_wg;
+    a.mq_cut = at<int32_t>(c->d_step, c->off_cut);
+    a.n_cut = c->st_mq_cut;
     a.num_heads = c->cfg.num_heads;
     a.num_kv_heads = c->cfg.num_kv_heads;
     a.tree = tree ? 1 : 0;

@@ -240,6 +240,12 @@ struct MultiQueryArgs {
     const uint64_t *tok_bits; // device [T] (tree mode) or null
     const int32_t *upre;      // device [n_seqs+1]: tiles of earlier sequences (units of one head)
     const int32_t *mq_pre;    // device [n_units+1]: positions of earlier units (blocks + mq_unit_cost each)
+    // Device [n_cut][kMqCutWords]: the units cut across workgroups, as
+    // kva_step_begin found them from the shares of n_wg (head, first new
+    // token of the tile, its valid tokens, first and last share, first
+    // piece's slot); the combine launch has one row of workgroups per cut unit.
+    const int32_t *mq_cut;
+    int32_t n_cut;
     int32_t n_seqs;
     int32_t n_units;          // (kv head, sequence, token tile) units, head-major
     int32_t total_blocks;     // positions of all units (blocks + mq_unit_cost each)
@@ -277,6 +283,17 @@ constexpr int mq_keys_for(int waves, bool tree_plan) { return (waves == 8 && !tr
 constexpr int mq_unit_cost(int keys) { return 128 / keys; }
 constexpr int kMqMaxGroup = 8;    // largest GQA group of the multi-query kernel
 constexpr int kMqSlotRows = 128;  // query rows of a partial slot (waves x 16 x tiles at most)
+constexpr int kMqCutWords = 8;    // int32 words of a cut-unit record (6 used)
+// Workgroups of a multi-query launch over `blocks` positions: one per CU (the
+// cap), at least 128 keys' blocks each.  kva_step_begin (the cut-unit
+// records) and the launch must agree.
+inline int32_t mq_wg_count(int64_t blocks, int32_t keys, int32_t cap) {
+    const int64_t min_blocks = 128 / keys;
+    const int64_t w = (blocks + min_blocks - 1) / min_blocks;
+    return static_cast<int32_t>(w < 1 || cap < 1 ? 1 : (w > cap ? cap : w));
+}
+// First position of share w of W over n positions (the device's mq_wg_start).
+inline int32_t mq_share_start(int64_t w, int64_t n, int64_t W) { return static_cast<int32_t>(w * n / W); }
 // A unit's query rows are (token, head) pairs of the GQA group, 16 per
 // MFMA tile, n_t tiles per wave: tokens per unit tile.
 constexpr int mq_tile_tokens(int G, int n_waves, int n_t) { return 16 * n_waves * n_t / G; }
