@@ -12,10 +12,13 @@ over L_b+1 rows).
 
 Prints ONE JSON line.  ``value`` is the KV bytes the decode attention reads
 per second over the whole timed region (the metric's "decode-attn KV-read
-HBM GB/s"); ``tok_per_s`` is sequences x steps / time.  ``roofline`` is the
-decode kernel alone: algorithmic bytes per launch (KV rows read + queries)
-over its average duration from HIP events recorded on the launch stream
-around each decode launch inside the timed region.  ``cpu_baseline`` is the
+HBM GB/s"); ``tok_per_s`` is sequences x steps / time.  The timed steps
+carry no events (a marker costs the stream about 3 us).  ``roofline`` is one
+kva_decode call: algorithmic bytes per launch (KV rows read + queries) over
+its average duration, from HIP events recorded on the launch stream around
+the 16 decode calls of each of as many further steps (their appends run
+first), divided by 16; ``roofline.decode_kernel`` is the decode kernel
+alone, from the library's events around each launch.  ``cpu_baseline`` is the
 numpy oracle on a bounded sample of the same workload on this host.
 The default line also carries the fixed ctx=8192 case (``ctx8192``), the
 measured read and copy ceilings (``peaks``) and every other workload's own
@@ -155,22 +158,30 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
     seqs = list(range(B))
     ones = [1] * B
 
-    def step(ev_pairs=None, kernel=False):
-        # ev_pairs: per layer, events around the kva_decode call, or (kernel)
-        # the library's events around the decode kernel alone.
+    def step(bracket=None, ev_pairs=None):
+        # Plain: each layer's append, then its decode, no events (the timed
+        # steps: an event marker costs the stream about 3 us, 95 us per step
+        # when every call was bracketed).  bracket: the step's appends, then
+        # its 16 decode calls between one pair of events (the per-call figure
+        # is the pair's time over 16).  ev_pairs: the library's events around
+        # each decode kernel alone (kva_kernel_events).
         for b in seqs:
             cache.set_len(b, int(lengths[b]))
         cache.begin_step(seqs, ones)
+        if bracket is not None:
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
+            bracket[0].record()
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+                cache.decode(layer, q, out)
+            bracket[1].record()
+            return
         for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
             cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
-            if ev_pairs is not None and kernel:
+            if ev_pairs is not None:
                 cache.kernel_events(ev_pairs[layer][0], ev_pairs[layer][1])
-            elif ev_pairs is not None:
-                ev_pairs[layer][0].record()
             cache.decode(layer, q, out)
-            if ev_pairs is not None and not kernel:
-                ev_pairs[layer][1].record()
-        if kernel:
+        if ev_pairs is not None:
             cache.kernel_events(None, None)
 
     log(f"{label}: B={B} sum_ctx={int(np.sum(lengths)) + B} warmup={warmup}")
@@ -178,24 +189,26 @@ def decode_workload(dev, lengths, block_ids, n_blocks, steps, warmup, split, lab
         step()
     dev.synchronize()
     split_used, n_splits = cache.decode_split()
-    evs = [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
-        step(evs[i])
+        step()
     dev.synchronize()
     wall = time.perf_counter() - t0
-    dec_ms = [e[0].elapsed_ms(e[1]) for per_step in evs for e in per_step]
-    # The decode kernel's own duration, in steps of their own: two more event
-    # markers inside each call add a few us to it, so they stay out of the
-    # steps the call bracket and the step time come from.
+    # The per-call figure and the decode kernel's own duration, in steps of
+    # their own after the timed ones.
+    brackets = [[Event(), Event()] for _ in range(steps)]
     for i in range(steps):
-        step(evs[i], kernel=True)
+        step(bracket=brackets[i])
+    dev.synchronize()
+    dec_ms = [p[0].elapsed_ms(p[1]) / LAYERS for p in brackets]
+    evs = [[[Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
+    for i in range(steps):
+        step(ev_pairs=evs[i])
     dev.synchronize()
     ker_ms = [e[0].elapsed_ms(e[1]) for per_step in evs for e in per_step]
-    for per_step in evs:
-        for pair in per_step:
-            for x in pair:
-                x.destroy()
+    for pair in brackets + [pair for per_step in evs for pair in per_step]:
+        for x in pair:
+            x.destroy()
     log(f"{label}: {steps} steps in {wall * 1e3:.2f} ms; kva_decode avg {np.mean(dec_ms) * 1e3:.1f} us, "
         f"decode kernel avg {np.mean(ker_ms) * 1e3:.1f} us")
     tl = None
@@ -280,34 +293,44 @@ def proj_workload(dev, steps, warmup, hidden=5120):
     seqs, ones = list(range(B)), [1] * B
 
     def step(evs=None):
+        # The 16 layers' projections, then their gated decodes, then their
+        # O-projections (each layer has its own buffers), each group between
+        # one pair of events: a per-call figure is the group's time over 16
+        # (an event marker costs the stream about 3 us, too much to put one
+        # around every call).
         for b in seqs:
             cache.set_len(b, int(lengths[b]))
         cache.begin_step(seqs, ones)
+        if evs is not None:
+            evs[0].record()
         for layer, (x, wq, wkv, wo, qw, kw, q, g, out) in enumerate(layers):
-            if evs is not None:
-                evs[layer][0].record()
             cache.project_append(layer, x, hidden, wq, wkv, qw, kw, d_cos, d_sin, rows, q, g)
-            if evs is not None:
-                evs[layer][1].record()
+        if evs is not None:
+            evs[1].record()
+        for layer, (x, wq, wkv, wo, qw, kw, q, g, out) in enumerate(layers):
             cache.decode(layer, q, out, gate=g)
-            if evs is not None:
-                evs[layer][2].record()
+        if evs is not None:
+            evs[2].record()
+        for layer, (x, wq, wkv, wo, qw, kw, q, g, out) in enumerate(layers):
             cache.out_project(out, B, q_dim, wo, hidden, x, residual=x)  # hidden += o_proj(attn)
-            if evs is not None:
-                evs[layer][3].record()
+        if evs is not None:
+            evs[3].record()
 
     for _ in range(warmup):
         step()
     dev.synchronize()
-    evs = [[[Event(), Event(), Event(), Event()] for _ in range(LAYERS)] for _ in range(steps)]
+    evs = [[Event(), Event(), Event(), Event()] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
         step(evs[i])
     dev.synchronize()
     wall = time.perf_counter() - t0
-    proj_ms = [e[0].elapsed_ms(e[1]) for s_ in evs for e in s_]
-    dec_ms = [e[1].elapsed_ms(e[2]) for s_ in evs for e in s_]
-    out_ms = [e[2].elapsed_ms(e[3]) for s_ in evs for e in s_]
+    proj_ms = [e[0].elapsed_ms(e[1]) / LAYERS for e in evs]
+    dec_ms = [e[1].elapsed_ms(e[2]) / LAYERS for e in evs]
+    out_ms = [e[2].elapsed_ms(e[3]) / LAYERS for e in evs]
+    for e in evs:
+        for x in e:
+            x.destroy()
     cache.destroy()
     alg = (nq + nkv) + B * hidden * 2 + 2 * B * H * D * 2 + B * 2 * HKV * D * 2
     alg_out = no + B * q_dim * 2 + 2 * B * hidden * 2  # W_o, attention rows, hidden read + written
@@ -604,30 +627,36 @@ def c4_workload(dev, steps, warmup, extras=True):
     seqs = list(range(B))
 
     def step(evs=None, kernel=False, mode="fused"):
-        # fused: kva_append_prefill (append + attention, one call) in the
-        # bracket; two: kva_append_qknorm_rope + kva_prefill in the bracket;
-        # prefill: kva_prefill alone, the append before the bracket (how
-        # earlier lines were measured).
+        # The 16 layers' calls between one pair of events, evs[0] (per call:
+        # the pair's time over 16; an event marker costs the stream about
+        # 3 us).  fused: kva_append_prefill (append + attention, one call);
+        # two: kva_append_qknorm_rope + kva_prefill; prefill: kva_prefill
+        # alone, the appends before the pair (how earlier lines were
+        # measured).  kernel: each layer's fused call with the library's
+        # events (evs[layer]) around mq_kernel alone.
         for b in seqs:
             cache.set_len(b, prefix[b])
         cache.begin_step(seqs, chunk)
-        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
-            if mode == "prefill":
+        if kernel:
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+                cache.kernel_events(evs[layer][0], evs[layer][1])
+                cache.append_prefill(layer, q, k, v, qw, kw, d_cos, d_sin, 4096, out)
+            cache.kernel_events(None, None)
+            return
+        if mode == "prefill":
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
                 cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
-            if evs is not None and kernel:
-                cache.kernel_events(evs[layer][0], evs[layer][1])  # mq_kernel alone
-            elif evs is not None:
-                evs[layer][0].record()
+        if evs is not None:
+            evs[0][0].record()
+        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
             if mode == "fused":
                 cache.append_prefill(layer, q, k, v, qw, kw, d_cos, d_sin, 4096, out)
             else:
                 if mode == "two":
                     cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
                 cache.prefill(layer, q, out)
-            if evs is not None and not kernel:
-                evs[layer][1].record()
-        if kernel:
-            cache.kernel_events(None, None)
+        if evs is not None:
+            evs[0][1].record()
 
     for _ in range(warmup):
         step()
@@ -648,7 +677,8 @@ def c4_workload(dev, steps, warmup, extras=True):
             dev.synchronize()
             if m == modes[0]:
                 wall += time.perf_counter() - t0
-    per = {m: [e[0].elapsed_ms(e[1]) for s in evs[m] for e in s] for m in modes}
+    per = {m: ([e[0].elapsed_ms(e[1]) for s in evs[m] for e in s] if m[1] else
+               [s[0][0].elapsed_ms(s[0][1]) / LAYERS for s in evs[m]]) for m in modes}
     ms = per[modes[0]]
     kms, two_ms, pre_ms = (per[m] for m in modes[1:]) if extras else (None, None, None)
     for m in modes:
@@ -700,46 +730,53 @@ def c5_workload(dev, steps, warmup, layers=4, batch=64):
     keep = [tr.root_to_node_path(wl.C5_PARENTS, int(n)) for n in accept]
     seqs = list(range(batch))
 
-    def step(evs=None, kernel=False):
+    def step(evs=None, kernel_evs=None):
+        # evs: the step's appends, then its tree-verify calls between one
+        # pair of events (per call: the pair's time over the layers), then
+        # the rollback between another pair.  kernel_evs: each layer's append
+        # and verify, with the library's events around mq_kernel alone.
         for b in seqs:
             cache.set_len(b, lengths[b])
         cache.begin_step(seqs, [9] * batch, rope_pos=rope_pos, tree_bits=bits)
-        for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
-            cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
-            if evs is not None and kernel:
-                cache.kernel_events(evs[layer][0], evs[layer][1])  # mq_kernel alone
-            elif evs is not None:
-                evs[layer][0].record()
-            cache.tree_verify(layer, q, out)
-            if evs is not None and not kernel:
-                evs[layer][1].record()
-        if kernel:
+        if kernel_evs is not None:
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
+                cache.kernel_events(kernel_evs[layer][0], kernel_evs[layer][1])
+                cache.tree_verify(layer, q, out)
             cache.kernel_events(None, None)
+        else:
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, rows)
+            if evs is not None:
+                evs[0].record()
+            for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
+                cache.tree_verify(layer, q, out)
+            if evs is not None:
+                evs[1].record()
         if evs is not None:
-            evs[layers][0].record()
+            evs[2].record()
         cache.rollback(seqs, lengths, keep)
         if evs is not None:
-            evs[layers][1].record()
+            evs[3].record()
 
     for _ in range(warmup):
         step()
     dev.synchronize()
-    evs = [[[Event(), Event()] for _ in range(layers + 1)] for _ in range(steps)]
+    evs = [[Event() for _ in range(4)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
         step(evs[i])
     dev.synchronize()
     wall = time.perf_counter() - t0
-    verify_ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s[:layers]]
-    rb_ms = [s[layers][0].elapsed_ms(s[layers][1]) for s in evs]
+    verify_ms = [e[0].elapsed_ms(e[1]) / layers for e in evs]
+    rb_ms = [e[2].elapsed_ms(e[3]) for e in evs]
+    kevs = [[[Event(), Event()] for _ in range(layers)] for _ in range(steps)]
     for i in range(steps):  # mq_kernel's own duration, in steps of their own
-        step(evs[i], kernel=True)
+        step(kernel_evs=kevs[i])
     dev.synchronize()
-    kernel_ms = [e[0].elapsed_ms(e[1]) for s in evs for e in s[:layers]]
-    for s in evs:
-        for pair in s:
-            for x in pair:
-                x.destroy()
+    kernel_ms = [e[0].elapsed_ms(e[1]) for s in kevs for e in s]
+    for x in [x for e in evs for x in e] + [x for s in kevs for pair in s for x in pair]:
+        x.destroy()
     cache.destroy()
     kv = sum(lengths) * ROW_BYTES + T * ROW_BYTES
     return {"wall_s": wall, "steps": steps, "layers": layers, "kv_bytes_per_layer": kv,
@@ -1001,6 +1038,8 @@ def workload_line(dev, args) -> dict:
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("project_c3_traffic.json"),
                          "kernel": "kva_project_append = proj_lds_kernel<2 token tiles, 8 waves, 7 row tiles, "
                                    "10 k-steps, 6 stages> + proj_finish_kernel",
+                         "timing": "HIP events around each step's 16 projections (then its 16 gated decodes, then "
+                                   "its 16 O-projections, each group between its own pair), over 16",
                          "avg_us": r["proj_avg_us"], "alg_bytes_per_launch": r["alg_bytes_proj"]}})
     if args.workload == "proj4":
         r = proj_prefill_workload(dev, args.steps, args.warmup)
@@ -1034,6 +1073,8 @@ def workload_line(dev, args) -> dict:
                          "frac": tflops / MFMA_PEAK_TFLOPS, "traffic": load_traffic("prefill_c4_traffic.json"),
                          "kernel": "kva_append_prefill = append_kernel + mq_kernel<1 tile, 8 waves, causal, "
                                    "64-key blocks> + mq_combine_kernel",
+                         "timing": "HIP events around each step's 16 calls (caches flushed before the step), "
+                                   "over 16; the modes take turns step by step",
                          "two_calls_avg_us": r["two_calls_avg_us"],
                          "prefill_only_avg_us": r["prefill_only_avg_us"],
                          "mq_kernel": {"what": "mq_kernel alone: HIP events the library records around its launch "
@@ -1058,6 +1099,7 @@ def workload_line(dev, args) -> dict:
             "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": load_traffic("tree_c5_traffic.json"),
                          "kernel": "kva_tree_verify = mq_kernel<1 tile, 4 waves, tree, 32-key blocks> + mq_combine_kernel",
+                         "timing": "HIP events around each step's verify calls (its appends first), over the layers",
                          "mq_kernel": {"what": "mq_kernel alone: HIP events the library records around its launch "
                                                "(kva_kernel_events), in a second set of as many steps",
                                        "avg_us": r["kernel_avg_us"], "achieved": kernel_gbs,
@@ -1196,8 +1238,8 @@ def decode_line(dev, which, args):
                      "traffic_source": f"profiles/{traffic_file}: rocprofv3 FETCH_SIZE and WRITE_SIZE of this "
                                        "workload (separate runs), scaled by the copy-kernel calibration stored "
                                        "there; a stored figure, not counted in this run",
-                     "kernel": "kva_decode = decode_mfma_kernel<6> (stream-K, QK on MFMA) + combine_kernel<6> (one stream, "
-                               "HIP events around the call)",
+                     "kernel": "kva_decode = decode_mfma_kernel<6> (stream-K, QK on MFMA) + combine_kernel<6> (one stream; "
+                               "HIP events around each step's 16 calls, after its appends, over 16)",
                      "avg_us": r["decode_avg_us"],
                      "alg_bytes_per_launch": r["alg_bytes_decode_launch"],
                      "decode_kernel": {"what": "decode_mfma_kernel<6> alone: HIP events the library records right "
