@@ -627,13 +627,15 @@ def c4_workload(dev, steps, warmup, extras=True):
     seqs = list(range(B))
 
     def step(evs=None, kernel=False, mode="fused"):
-        # The 16 layers' calls between one pair of events, evs[0] (per call:
-        # the pair's time over 16; an event marker costs the stream about
-        # 3 us).  fused: kva_append_prefill (append + attention, one call);
-        # two: kva_append_qknorm_rope + kva_prefill; prefill: kva_prefill
-        # alone, the appends before the pair (how earlier lines were
-        # measured).  kernel: each layer's fused call with the library's
-        # events (evs[layer]) around mq_kernel alone.
+        # fused: kva_append_prefill (append + attention, one call); two:
+        # kva_append_qknorm_rope + kva_prefill; the 16 layers' calls between
+        # one pair of events, evs[0] (per call: the pair's time over 16; an
+        # event marker costs the stream about 3 us).  prefill: each layer's
+        # append, then its kva_prefill between a pair of its own, evs[layer]
+        # (how earlier lines were measured: the append just before leaves q
+        # in the caches, which running all appends first would not).
+        # kernel: each layer's fused call with the library's events
+        # (evs[layer]) around mq_kernel alone.
         for b in seqs:
             cache.set_len(b, prefix[b])
         cache.begin_step(seqs, chunk)
@@ -646,14 +648,19 @@ def c4_workload(dev, steps, warmup, extras=True):
         if mode == "prefill":
             for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
                 cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
+                if evs is not None:
+                    evs[layer][0].record()
+                cache.prefill(layer, q, out)
+                if evs is not None:
+                    evs[layer][1].record()
+            return
         if evs is not None:
             evs[0][0].record()
         for layer, (q, k, v, qw, kw, out) in enumerate(inputs):
             if mode == "fused":
                 cache.append_prefill(layer, q, k, v, qw, kw, d_cos, d_sin, 4096, out)
             else:
-                if mode == "two":
-                    cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
+                cache.append(layer, q, k, v, qw, kw, d_cos, d_sin, 4096)
                 cache.prefill(layer, q, out)
         if evs is not None:
             evs[0][1].record()
@@ -677,7 +684,7 @@ def c4_workload(dev, steps, warmup, extras=True):
             dev.synchronize()
             if m == modes[0]:
                 wall += time.perf_counter() - t0
-    per = {m: ([e[0].elapsed_ms(e[1]) for s in evs[m] for e in s] if m[1] else
+    per = {m: ([e[0].elapsed_ms(e[1]) for s in evs[m] for e in s] if m[1] or m[0] == "prefill" else
                [s[0][0].elapsed_ms(s[0][1]) / LAYERS for s in evs[m]]) for m in modes}
     ms = per[modes[0]]
     kms, two_ms, pre_ms = (per[m] for m in modes[1:]) if extras else (None, None, None)
@@ -1077,6 +1084,8 @@ def workload_line(dev, args) -> dict:
                                    "over 16; the modes take turns step by step",
                          "two_calls_avg_us": r["two_calls_avg_us"],
                          "prefill_only_avg_us": r["prefill_only_avg_us"],
+                         "prefill_only_timing": "each layer's append, then its kva_prefill between a pair of "
+                                                "events of its own (the pair's markers in the figure)",
                          "mq_kernel": {"what": "mq_kernel alone: HIP events the library records around its launch "
                                                "(kva_kernel_events), in a second set of as many steps",
                                        "avg_us": r["kernel_avg_us"], "achieved": kernel_tflops,
