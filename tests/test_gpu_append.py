@@ -23,15 +23,28 @@ def _bits(a):
     return np.ascontiguousarray(a).view(np.uint16)
 
 
-@pytest.mark.parametrize("rope_override", [False, True])
-def test_append_bitexact_with_canary(device, rope_override):
+@pytest.mark.parametrize("rope_override,many", [(False, False), (True, False), (False, True), (True, True)])
+def test_append_bitexact_with_canary(device, rope_override, many):
+    """42 tokens, or (many) 306 tokens over 20 permuted blocks of four
+    sequences, with RoPE positions from the slots or overridden."""
     rng = np.random.default_rng(21)
-    lengths = [0, 37, 250, 16]
-    n_new = [1, 5, 20, 16]
-    ids = [[9, 2], [4, 11, 0], [13, 7, 1, 15, 5, 12, 3, 8, 10, 14, 6, 16, 17, 18, 19, 20, 21],
-           [22, 23]]
-    say(f"append canary rope_override={rope_override}")
-    cache, _, _ = build_cache(lengths, ids, extra_rows=n_new, n_layers=2, rng=rng, max_blocks=24)
+    if many:
+        lengths, n_new = [0, 37, 250, 16], [1, 5, 200, 100]
+        nblk = [(L + n + 15) // 16 for L, n in zip(lengths, n_new)]
+        perm = [int(x) for x in rng.permutation(sum(nblk) + 3)]
+        ids, o = [], 0
+        for n in nblk:
+            ids.append(perm[o:o + n])
+            o += n
+        max_blocks = sum(nblk) + 3
+    else:
+        lengths = [0, 37, 250, 16]
+        n_new = [1, 5, 20, 16]
+        ids = [[9, 2], [4, 11, 0], [13, 7, 1, 15, 5, 12, 3, 8, 10, 14, 6, 16, 17, 18, 19, 20, 21],
+               [22, 23]]
+        max_blocks = 24
+    say(f"append canary rope_override={rope_override} many={many}")
+    cache, _, _ = build_cache(lengths, ids, extra_rows=n_new, n_layers=2, rng=rng, max_blocks=max_blocks)
     tables = Tables(device, 1024)
     T = sum(n_new)
     q = rng.standard_normal((T, H, D), dtype=np.float32).astype(np.float16)
