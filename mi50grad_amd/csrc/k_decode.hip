@@ -654,24 +654,32 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs 
     const int h = u - b * hkv;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    int P, W;
-    stream_k_shape(a, P, W);
-    const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
-    const int npg = (ctx + 15) >> 4;
-    if (npg == 0) return;
-    const int first = seq_page_base(a, b, npg);
-    const int w0 = wg_of_page<true>(first, P, W);
-    const int w1 = wg_of_page<true>(first + npg - 1, P, W);
-    if (w0 == w1) return;  // one workgroup covered the sequence and wrote it
-    const int n = w1 - w0 + 1;
-    const int nw = blockDim.x >> 6;  // 1 when the host knows no sequence has more than kChunk pieces
-    const bool multi = n > kChunk;   // uniform over the workgroup
-    if (!multi && wave != 0) return;
     // Partial i comes from workgroup w0 + i: slot 2w when the sequence began
     // at or before that workgroup's range, else 2w+1.  Only w0's range can
     // begin after the sequence's first page, so one division settles every
     // slot (one per piece kept the pieces' loads from going out together).
-    const int slot0 = 2 * w0 + (first <= wg_start<true>(w0, P, W) ? 0 : 1);
+    int w0, n, slot0;
+    if (a.n_crec > 0) {  // the host's figures, with the kernel arguments
+        w0 = a.crec[b];
+        if (w0 < 0) return;  // one workgroup covered the sequence and wrote it
+        n = a.crec_n[b] >> 1;
+        slot0 = 2 * w0 + (a.crec_n[b] & 1);
+    } else {
+        int P, W;
+        stream_k_shape(a, P, W);
+        const int ctx = a.ctx_lens ? a.ctx_lens[b] : a.ctx_len_const;
+        const int npg = (ctx + 15) >> 4;
+        if (npg == 0) return;
+        const int first = seq_page_base(a, b, npg);
+        w0 = wg_of_page<true>(first, P, W);
+        const int w1 = wg_of_page<true>(first + npg - 1, P, W);
+        if (w0 == w1) return;  // one workgroup covered the sequence and wrote it
+        n = w1 - w0 + 1;
+        slot0 = 2 * w0 + (first <= wg_start<true>(w0, P, W) ? 0 : 1);
+    }
+    const int nw = blockDim.x >> 6;  // 1 when the host knows no sequence has more than kChunk pieces
+    const bool multi = n > kChunk;   // uniform over the workgroup
+    if (!multi && wave != 0) return;
     auto row_of = [&](int i) -> size_t {
         const int slot = i == 0 ? slot0 : 2 * (w0 + i);
         return (static_cast<size_t>(slot) * hkv + h) * G + g;

@@ -119,6 +119,7 @@ struct kva_cache {
     int32_t st_mq_q = 0;         // new tokens per unit tile
     size_t off_upre = 0, off_mqpre = 0;
     bool st_all_one = false, st_has_bits = false;
+    std::vector<int32_t> st_pre;  // pages of the step's earlier sequences, [n_seqs + 1]
     size_t off_seq = 0, off_ctx = 0, off_start = 0, off_tokoff = 0, off_tseq = 0,
            off_tslot = 0, off_tpos = 0, off_bits = 0, off_pre = 0, off_pids = 0, off_cut = 0;
 
@@ -835,6 +836,7 @@ int kva_step_begin(kva_cache *c, int32_t n_seqs, const int32_t *seq_ids, const i
     c->off_upre = o_upre;
     c->off_mqpre = o_mqpre;
     c->st_all_one = all_one;
+    c->st_pre.assign(p_pre, p_pre + n_seqs + 1);
     c->st_has_bits = tree_bits != nullptr;
     c->step_valid = true;
     return KVA_OK;
@@ -1071,6 +1073,30 @@ static int32_t combine_waves_for(int64_t max_npg, int64_t pages, int32_t n_wg) {
     return max_npg * n_wg / pages + 2 <= kva::kCombineChunk ? 1 : 4;
 }
 
+// The combine's per-sequence facts for a launch of a.n_wg shares over
+// a.total_pages pages (pre: the pages of earlier sequences), computed as the
+// kernels split the pages: share w starts at w*P/W.
+static void set_combine_recs(const std::vector<int32_t> &pre, kva::DecodeArgs &a) {
+    a.n_crec = 0;
+    const int32_t n = a.n_seqs;
+    if (n > kva::kCombineRecs || static_cast<int64_t>(pre.size()) != static_cast<int64_t>(n) + 1) return;
+    const int64_t P = a.total_pages, W = a.n_wg;
+    if (P <= 0 || W <= 0) return;
+    auto start = [&](int64_t w) { return w * P / W; };
+    auto wg_of = [&](int64_t p) {
+        int64_t w = p * W / P;
+        while (w + 1 < W && start(w + 1) <= p) ++w;
+        return w;
+    };
+    for (int32_t b = 0; b < n; ++b) {
+        const int64_t first = pre[b], npg = pre[b + 1] - pre[b];
+        const int64_t w0 = npg > 0 ? wg_of(first) : 0, w1 = npg > 0 ? wg_of(first + npg - 1) : 0;
+        a.crec[b] = (npg > 0 && w0 != w1) ? static_cast<int32_t>(w0) : -1;
+        a.crec_n[b] = static_cast<int32_t>(2 * (w1 - w0 + 1) + (first <= start(w0) ? 0 : 1));
+    }
+    a.n_crec = n;
+}
+
 static void set_stream_k(kva_cache *c, kva::DecodeArgs &a, int64_t pages, int32_t num_heads) {
     a.total_pages = static_cast<int32_t>(pages);
     // Two partial slots of num_heads rows per workgroup must fit the workspace.
@@ -1164,6 +1190,7 @@ static int decode_impl(kva_cache *c, int32_t layer, const void *q, const void *g
     } else {
         a.combine_waves = combine_waves_for((c->st_max_ctx + kva::kBlockTokens - 1) / kva::kBlockTokens,
                                             a.total_pages, a.n_wg);
+        set_combine_recs(c->st_pre, a);
     }
     a.out = static_cast<uint16_t *>(out);
     a.ev_before = c->kev_before;

@@ -14,6 +14,7 @@ constexpr int kHeadDim = 256;     // the only head_dim the paged kernels take
 constexpr int kBlockTokens = 16;  // tokens per page
 constexpr int kDecodeHeadsPerWg = 4;  // kv heads per stream-K decode workgroup (one wave each), at most
 constexpr int kSplitQuantum = 16; // decode split sizes are whole pages
+constexpr int kCombineRecs = 64;  // sequences whose combine facts travel in the decode arguments
 constexpr int kPlanPages = 64;    // page ids per sequence in the step plan (one per lane)
 constexpr int kCombineChunk = 16; // decode partials a combine wave requests together
 
@@ -156,6 +157,14 @@ struct DecodeArgs {
     // 1: the combine launch gets one wave per workgroup (the host has shown
     // that no sequence is cut into more than kCombineChunk pieces); else four.
     int32_t combine_waves;
+    // The combine's view of each sequence, in the kernel arguments so its
+    // first loads are the partials (n_crec = n_seqs <= kCombineRecs; 0: it
+    // reads the length from the step plan and derives these): crec[b] = the
+    // workgroup of the sequence's first piece, -1 when one workgroup covered
+    // it; crec_n[b] = 2 * pieces + 1 if the first piece's slot is 2*w0 + 1.
+    int32_t n_crec;
+    int32_t crec[kCombineRecs];
+    int32_t crec_n[kCombineRecs];
     float *ws_acc;            // [2*n_wg][Hkv][G][256] partial slots
     float *ws_ml;             // [2*n_wg][Hkv][G][2]
     uint16_t *out;            // [n_seqs][H][256]
