@@ -8,10 +8,14 @@ return code: hip_dispatch.py:267-269).  The library must have been built
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().with_name("libkvattn.so")
+# KVA_LIB names another build of the library (the host-sanitized one of
+# `python -m mi50grad_amd.build --sanitize`); by default the in-tree build.
+LIB_PATH = Path(os.environ["KVA_LIB"]).resolve() if os.environ.get("KVA_LIB") \
+    else Path(__file__).resolve().with_name("libkvattn.so")
 
 KVA_FLAG_HOST_ONLY = 0x1
 ERROR_NAMES = {

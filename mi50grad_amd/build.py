@@ -4,6 +4,13 @@ hipcc compiles the kernels (``csrc/k_*.hip``) for gfx950 only; g++ compiles the
 host side (``csrc/kva_host.cpp``) against the HIP runtime API; hipcc links the
 shared library in-tree (``mi50grad_amd/libkvattn.so``) so it travels with the
 source tree.  The build always recompiles: it is the "does it build" check.
+
+``--sanitize`` builds ``libkvattn_san.so`` instead: the same kernels, the host
+side under AddressSanitizer and UndefinedBehaviorSanitizer (g++ only; no GPU
+code is instrumented).  The CPU suite runs against it with
+
+    ASAN_OPTIONS=detect_leaks=0 LD_PRELOAD=$(gcc -print-file-name=libasan.so) \
+        KVA_LIB=mi50grad_amd/libkvattn_san.so python -m pytest tests -m "not gpu"
 """
 from __future__ import annotations
 
@@ -19,6 +26,7 @@ CSRC = PKG / "csrc"
 ROOT = PKG.parent
 INCLUDE = ROOT / "include"
 OUT = PKG / "libkvattn.so"
+OUT_SAN = PKG / "libkvattn_san.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
@@ -33,6 +41,7 @@ HOST_FLAGS = [
     "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
     "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
+SAN_FLAGS = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-g"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -41,16 +50,18 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every kernel and the host side, link libkvattn.so; return its path."""
-    objdir = PKG / "_build"
+def build(verbose: bool = False, sanitize: bool = False) -> Path:
+    """Compile every kernel and the host side, link libkvattn.so (sanitize:
+    libkvattn_san.so, host side instrumented); return its path."""
+    objdir = PKG / ("_build_san" if sanitize else "_build")
+    out = OUT_SAN if sanitize else OUT
     if objdir.exists():
         shutil.rmtree(objdir)
     objdir.mkdir()
     jobs = []
     for src in sorted(CSRC.glob("k_*.hip")):
         jobs.append([HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(objdir / (src.stem + ".o"))])
-    jobs.append(["g++", *HOST_FLAGS, "-c", str(CSRC / "kva_host.cpp"),
+    jobs.append(["g++", *HOST_FLAGS, *(SAN_FLAGS if sanitize else []), "-c", str(CSRC / "kva_host.cpp"),
                  "-o", str(objdir / "kva_host.o")])
     with cf.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
         for cmd, fut in zip(jobs, [ex.submit(_run, j) for j in jobs]):
@@ -58,14 +69,18 @@ def build(verbose: bool = False) -> Path:
                 print(" ".join(cmd))
             fut.result()
     objs = sorted(str(p) for p in objdir.glob("*.o"))
-    tmp = OUT.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs,
-          f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"])
-    os.replace(tmp, OUT)
+    tmp = out.with_suffix(".so.tmp")
+    if sanitize:  # the instrumented host object needs the sanitizer runtimes: link with g++
+        _run(["g++", "-shared", *SAN_FLAGS, "-o", str(tmp), *objs,
+              f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"])
+    else:
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs,
+              f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"])
+    os.replace(tmp, out)
     shutil.rmtree(objdir)
-    return OUT
+    return out
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, sanitize="--sanitize" in sys.argv)
     print(f"built {path}")
