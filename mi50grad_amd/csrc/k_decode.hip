@@ -345,13 +345,6 @@ __device__ __forceinline__ void load_page(Page &p, const char *kb, const char *v
     }
 }
 
-__device__ __forceinline__ void consume(const Page &p) {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) asm volatile("" ::"v"(p.k[s].x), "v"(p.k[s].y), "v"(p.k[s].z), "v"(p.k[s].w));
-#pragma unroll
-    for (int t = 0; t < kBlockTokens; ++t) asm volatile("" ::"v"(p.v[t].x), "v"(p.v[t].y));
-}
-
 // m: the running max of this lane's head column (raw scores), l: the fp16
 // probabilities of this lane's four rows summed, acc: dims 4l..4l+3 of every
 // head of the group.
