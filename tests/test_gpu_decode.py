@@ -92,6 +92,28 @@ def test_decode_ragged_permuted(device, split):
     cache.destroy()
 
 
+@pytest.mark.parametrize("B", [64, 65])
+def test_decode_combine_facts_boundary(device, B):
+    """Stream-K (64-token split) over 64 sequences, whose combine facts
+    travel in the launch arguments, and over 65, where the combine reads the
+    lengths from the step plan instead: both within 2e-3 of the oracle."""
+    rng = np.random.default_rng(900 + B)
+    lengths = [int(x) for x in rng.integers(90, 220, B)]
+    nblk = [(L + 1 + 15) // 16 for L in lengths]
+    perm = rng.permutation(sum(nblk))
+    ids, o = [], 0
+    for n in nblk:
+        ids.append([int(x) for x in perm[o:o + n]])
+        o += n
+    say(f"decode combine facts B={B}")
+    cache, kr, vr = build_cache(lengths, ids, extra_rows=1, rng=rng)
+    tables = Tables(device, 256)
+    got, exp, *_ = run_decode_step(device, cache, kr, vr, lengths, rng, tables, split=64)
+    assert cache.decode_split()[0] == 64
+    assert max_err(got, exp) <= TOL
+    cache.destroy()
+
+
 @pytest.mark.parametrize("split", [0, 16])
 def test_decode_short_steps(device, split):
     """A step whose longest sequence is at most 1024 rows: the automatic split
