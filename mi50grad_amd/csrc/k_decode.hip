@@ -634,19 +634,22 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void decode_mfma_kernel(DecodeArgs
 // leave).  A sequence cut into more pieces (one long sequence over every
 // CU) has its chunks dealt to the waves, which merge through LDS; with one
 // wave, it takes them all in turn.
+//
+// kHeads (the one-wave case): a workgroup per (sequence, kv head), its G
+// waves one query head each, so the launch has G times fewer workgroups.
 constexpr int kCombineWaves = 4;
-template <int G>
-__global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs a) {
+template <int G, bool kHeads = false>
+__global__ __launch_bounds__(64 * (kHeads ? G : kCombineWaves)) void combine_kernel(DecodeArgs a) {
     constexpr int kChunk = kCombineChunk;
     __shared__ float4 w_acc[kCombineWaves * 64];
     __shared__ float w_ml[kCombineWaves * 2];
     const int u = blockIdx.x;
-    const int g = blockIdx.y;
+    const int g = kHeads ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : static_cast<int>(blockIdx.y);
     const int hkv = a.num_kv_heads;
     const int b = u / hkv;
     const int h = u - b * hkv;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = kHeads ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // Partial i comes from workgroup w0 + i: slot 2w when the sequence began
     // at or before that workgroup's range, else 2w+1.  Only w0's range can
     // begin after the sequence's first page, so one division settles every
@@ -670,7 +673,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(DecodeArgs 
         n = w1 - w0 + 1;
         slot0 = 2 * w0 + (first <= wg_start<true>(w0, P, W) ? 0 : 1);
     }
-    const int nw = blockDim.x >> 6;  // 1 when the host knows no sequence has more than kChunk pieces
+    const int nw = kHeads ? 1 : blockDim.x >> 6;  // 1 when the host knows no sequence has more than kChunk pieces
     const bool multi = n > kChunk;   // uniform over the workgroup
     if (!multi && wave != 0) return;
     auto row_of = [&](int i) -> size_t {
@@ -1047,8 +1050,11 @@ hipError_t launch_g(const DecodeArgs &a, hipStream_t s) {
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(decode_mfma_kernel<G>, dim3(a.n_wg, a.num_kv_heads / hpw), dim3(64 * hpw), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess || (e = mark(a.ev_after, s)) != hipSuccess) return e;
-    const int cw = a.combine_waves == 1 ? 1 : kCombineWaves;
-    hipLaunchKernelGGL(combine_kernel<G>, dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * cw), 0, s, a);
+    if (a.combine_waves == 1)
+        hipLaunchKernelGGL((combine_kernel<G, true>), dim3(a.n_seqs * a.num_kv_heads), dim3(64 * G), 0, s, a);
+    else
+        hipLaunchKernelGGL((combine_kernel<G>), dim3(a.n_seqs * a.num_kv_heads, G), dim3(64 * kCombineWaves), 0, s,
+                           a);
     return hipGetLastError();
 }
 
