@@ -627,16 +627,17 @@ __global__ __launch_bounds__(64 * kMfmaWaves) void decode_mfma_kernel(DecodeArgs
 // cross-workgroup fences are needed: an agent-scope release on every decode
 // workgroup costs an L2 writeback per workgroup on multi-XCD parts.  The
 // (m, l) pairs and acc rows of up to kChunk partials are all requested before
-// any is used, so a sequence cut into at most kChunk pieces costs two memory
-// round trips (its length, then its partials), taken by wave 0 alone; when
-// the host can show that no sequence of the launch has more pieces, the
-// launch has one wave per workgroup (the other three would only start and
-// leave).  A sequence cut into more pieces (one long sequence over every
-// CU) has its chunks dealt to the waves, which merge through LDS; with one
-// wave, it takes them all in turn.
+// any is used, so a sequence cut into at most kChunk pieces costs one memory
+// round trip when the host passes each sequence's first piece and piece
+// count with the launch arguments (DecodeArgs::crec), two otherwise (its
+// length, then its partials).  A sequence cut into more pieces (one long
+// sequence over every CU) has its chunks dealt to the four waves of its
+// workgroup, which merge through LDS.
 //
-// kHeads (the one-wave case): a workgroup per (sequence, kv head), its G
-// waves one query head each, so the launch has G times fewer workgroups.
+// kHeads (the host has shown that no sequence of the launch has more than
+// kChunk pieces): a workgroup per (sequence, kv head), its G waves one
+// query head each, where the general form has a workgroup of four waves per
+// query head.
 constexpr int kCombineWaves = 4;
 template <int G, bool kHeads = false>
 __global__ __launch_bounds__(64 * (kHeads ? G : kCombineWaves)) void combine_kernel(DecodeArgs a) {
