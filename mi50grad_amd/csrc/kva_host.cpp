@@ -1063,11 +1063,11 @@ int kva_get_decode_split(const kva_cache *c, int32_t *split_tokens, int32_t *n_s
     return KVA_OK;
 }
 
-// Fill the stream-K fields of a decode launch over `pages` pages.
-// One wave per combine workgroup when no sequence can be cut into more than
-// kCombineChunk pieces (the combine's other waves only share the chunks of a
-// sequence cut into more): npg pages meet at most floor(npg * W / P) + 2 of
-// W shares of P pages.
+// The combine's form: 1 (a workgroup per sequence and kv head, a wave per
+// query head) when no sequence can be cut into more than kCombineChunk
+// pieces, else 4 (four waves per query head share the chunks of a sequence
+// cut into more): npg pages meet at most floor(npg * W / P) + 2 of W shares
+// of P pages.
 static int32_t combine_waves_for(int64_t max_npg, int64_t pages, int32_t n_wg) {
     if (pages <= 0) return 4;
     return max_npg * n_wg / pages + 2 <= kva::kCombineChunk ? 1 : 4;

@@ -154,8 +154,10 @@ struct DecodeArgs {
     int32_t dyn;
     int32_t split_tokens;     // 0 = one workgroup per CU up to the cap
     int32_t min_pages;
-    // 1: the combine launch gets one wave per workgroup (the host has shown
-    // that no sequence is cut into more than kCombineChunk pieces); else four.
+    // 1 (the host has shown that no sequence is cut into more than
+    // kCombineChunk pieces): the combine launch has a workgroup per
+    // (sequence, kv head) with a wave per query head; else a workgroup of
+    // four waves per (sequence, kv head, query head).
     int32_t combine_waves;
     // The combine's view of each sequence, in the kernel arguments so its
     // first loads are the partials (n_crec = n_seqs <= kCombineRecs; 0: it
